@@ -1,0 +1,126 @@
+/*
+ * tandem_w4.h - C ABI of the MI355X (gfx950) AWQ W4A16 linear library, libtandem_w4.so.
+ *
+ * y[M, N] = x[M, K] @ dequant(W)[N, K]^T with AutoAWQ 4-bit weights (group 128), fp16 activations,
+ * fp32 accumulation. Every pointer is a device pointer; every launch goes on the caller's HIP
+ * stream (`stream`, a hipStream_t passed as void*; NULL = the null stream). Launches allocate
+ * nothing, never synchronize and read no device memory from the host, so they may be captured
+ * in a HIP graph once tw4_init() has run for the device.
+ *
+ * Status: every entry point returns TW4_OK (0) or a nonzero TW4_E* code; tw4_last_error()
+ * returns the calling thread's last message (the reference raises RuntimeError from
+ * TORCH_CHECK with the same conditions, python/tandem/csrc/w4_gemv.cu:568-579).
+ *
+ * Weight layout ("tile layout", produced by tw4_repack_awq, consumed by every kernel):
+ *   packed  int32 [Npad/16][K/128][4 kb][16 r][4 s]   Npad = N rounded up to 16
+ *           word (kb, r, s) of row tile T and quant group g holds the 8 consecutive weights
+ *           k = 128 g + 32 kb + 8 s + o (o = 2 q + e, q = 0..3, e = 0..1) of row n = 16 T + r,
+ *           weight o in nibble q + 4 e. One row tile x one group is 1 KB: one 16-byte load per
+ *           lane of a 64-lane wavefront (lane 16 kb + r takes words s = 0..3). Rows n >= N
+ *           are zero.
+ *   scales  fp16 [N, K/128]    s[n, g]
+ *   zeros   fp16 [N, K/128]    z[n, g], the integer zero point (exact)
+ *   w[n, k] = fp16_rne((q[n, k] - z[n, k/128]) * s[n, k/128]).
+ * N is the number of output features (the rows of scales); packed must hold Npad * K / 8 words.
+ * The host view of `packed` is [Npad, K/8] int32: the same buffer size as the reference's
+ * post-finalize `packed` (python/tandem/layers/awq.py:49-68, 243-246), a different word order.
+ */
+#ifndef TANDEM_W4_H
+#define TANDEM_W4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TW4_OK = 0,
+    TW4_EINVAL = 1,    /* bad shape, alignment, size or argument */
+    TW4_ECONFIG = 2,   /* kernel configuration not compiled in */
+    TW4_EHIP = 3,      /* HIP runtime error (launch, attribute, device query) */
+    TW4_ESPACE = 4     /* split-K workspace or counters too small */
+};
+
+/* Library version string, e.g. "tandem_w4 0.1.0 gfx950". No reference counterpart (the
+ * reference's extension is a JIT torch module, python/tandem/layers/w4_cuda.py:44-62). */
+const char* tw4_version(void);
+
+/* Offload architecture the device code was compiled for ("gfx950"). */
+const char* tw4_arch(void);
+
+/* The calling thread's last error message ("" if none). Replaces the TORCH_CHECK messages of
+ * python/tandem/csrc/w4_gemv.cu:568-579, 599, 608, 624-625, 647, 654-661, 681. */
+const char* tw4_last_error(void);
+
+/* One-time set-up for `device`, before any graph capture: checks the device is gfx950, sets the
+ * dynamic-LDS limit of every GEMM configuration and records its occupancy for the last-wave
+ * split-K model. Replaces the first-launch static of gemm_launch (python/tandem/csrc/
+ * w4_gemv.cu:539-544) and the build-before-capture step of W4Linear.finalize
+ * (python/tandem/layers/awq.py:247-251). Safe to call repeatedly. */
+int tw4_init(int device);
+
+/* AutoAWQ "gemm" tensors -> tile layout, on the device.
+ *   qweight int32 [K, N/8], qzeros int32 [K/128, N/8] (AWQ nibble order 0,2,4,6,1,3,5,7),
+ *   scales fp16 [K/128, N]  ->  packed [Npad/16 * K/128 * 256] int32, scales_out / zeros_out
+ *   fp16 [N, K/128]. packed must be zero-filled by the caller (its rows >= N stay zero).
+ * interleave = 1 reorders rows as interleave_gate_up (gate rows 8T..8T+7 then up rows
+ * N/2+8T..N/2+8T+7 in row tile T; N % 16 == 0).
+ * Replaces repack_awq + interleave_gate_up (python/tandem/layers/awq.py:42-75, 235-241). */
+int tw4_repack_awq(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                   int32_t* packed, uint16_t* scales_out, uint16_t* zeros_out,
+                   int K, int N, int interleave, void* stream);
+
+/* Tile layout -> dense fp16 out [N, K] (nn.Linear layout), bit-exact fp16_rne((q - z) * s).
+ * deinterleave = 1 undoes interleave_gate_up on the rows. Replaces the Triton
+ * _w4_dequant_kernel / w4_dequant (python/tandem/layers/awq.py:89-133). */
+int tw4_dequant(const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                uint16_t* out, int N, int K, int deinterleave, void* stream);
+
+/* Decode GEMV on the vector ALUs, 1 <= M <= 4: y fp16 [M, N]. x fp16 [M, K] contiguous and
+ * 16-byte aligned. Config: warps_k wavefronts split K inside a workgroup, unroll quant groups
+ * in flight per lane, ntile row tiles (16 rows) per wavefront.
+ * Replaces w4_gemv (python/tandem/csrc/w4_gemv.cu:96-153, 581-617). */
+int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+             const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+             int warps_k, int unroll, int ntile, void* stream);
+
+/* Decode on the matrix cores (v_mfma_f32_16x16x32_f16, weights as the A operand, the batch on
+ * the 16-column side), 1 <= M <= 16. act = 1: y = silu(gate) * up, [M, N/2], rows in
+ * interleave_gate_up order (N % 16 == 0); act = 0: y [M, N].
+ * Replaces w4_mma (python/tandem/csrc/w4_gemv.cu:166-295, 619-648). */
+int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+            const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+            int warps_k, int unroll, int ntile, int act, void* stream);
+
+/* Fused-dequant GEMM for M > 16 (any M >= 1 works): x tiles double-buffered through LDS,
+ * weights dequantized in registers into MFMA fragments, fp32 accumulation, optional split-K
+ * across workgroups with a deterministic last-arriver reduction.
+ *   mt      16-token column tiles per workgroup (BM = 16 mt)
+ *   nt      16-row weight tiles per wavefront
+ *   warps_n wavefronts along N (BN = 16 nt warps_n)
+ *   warps_k wavefronts splitting each K step (1 or 2)
+ *   stages  LDS ring depth (2: double buffering)
+ *   splits  0: split only the last, partial wave of tiles along K; 1: no split; s > 1: every
+ *           tile split s ways
+ * ws (fp32, ws_floats) and locks (int32, n_locks, zero before the first call) are the split-K
+ * workspace; the kernel returns every counter to zero, so graph replays stay correct. Calls
+ * that share a workspace must not overlap.
+ * Replaces w4_gemm / gemm_launch (python/tandem/csrc/w4_gemv.cu:312-566, 650-683) and the
+ * workspace contract of python/tandem/layers/w4_cuda.py:24-41. */
+int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+             const uint16_t* zeros, uint16_t* y, float* ws, int32_t* locks,
+             int64_t ws_floats, int64_t n_locks, int M, int N, int K,
+             int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
+             void* stream);
+
+/* Grid the last tw4_gemm call on this thread launched: workgroups, data-parallel tiles and
+ * split factor (for benchmarks and tests; the reference keeps these internal,
+ * python/tandem/csrc/w4_gemv.cu:545-563). */
+int tw4_gemm_last_grid(int* blocks, int* dp_tiles, int* splits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TANDEM_W4_H */

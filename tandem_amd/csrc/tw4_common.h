@@ -1,0 +1,142 @@
+// Shared device helpers and host plumbing of libtandem_w4.so (gfx950 only).
+//
+// Tile layout (see include/tandem_w4.h): row tile T (16 rows) x quant group g is one 1 KB block
+// of 256 int32 words ordered [kb 4][r 16][s 4]; word (kb, r, s) holds weights
+// k = 128 g + 32 kb + 8 s + o of row 16 T + r, weight o = 2 q + e in nibble q + 4 e.
+// Lane l = 16 kb + r of a wavefront loads the 16 bytes (kb, r, s = 0..3) of a block with one
+// global_load_dwordx4, so a wavefront load of a block is 1 KB contiguous.
+//
+// The k order inside a word is the one that lets four v_and_or_b32 turn a word into four
+// half2 values with no integer-to-float conversion (the fp16 "magic number" trick: an fp16 with
+// bit pattern 0x6400 | m, m < 1024, has the value 1024 + m; published with FasterTransformer's
+// and Marlin's int4 dequantization). Pair q of the word, (weights 2q, 2q + 1), is nibbles
+// (q, q + 4): bits 4q .. 4q+3 and 16 + 4q .. 16 + 4q + 3.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tandem_w4.h"
+
+namespace tw4 {
+
+typedef _Float16 h1;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 128;       // quant group (k values per scale / zero)
+constexpr int kTileRows = 16;     // rows per row tile
+constexpr int kBlockWords = 256;  // int32 words per (row tile, group) block
+constexpr int kBlockU4 = 64;      // 16-byte vectors per block (one per lane)
+
+template <typename T, typename F>
+__device__ __forceinline__ T bitcast(F v) {
+    return __builtin_bit_cast(T, v);
+}
+
+// Per (row, group) constants of the in-register dequantization.
+struct GroupQ {
+    h2 zlo;  // -(1024 + z): subtracted from a low-nibble magic half (1024 + q)
+    h2 zhi;  // -(64 + z):   added to a high-nibble magic half times 1/16 ((1024 + 16 q) / 16)
+    h2 s;    // scale
+};
+
+__device__ __forceinline__ GroupQ group_q(h1 s, h1 z) {
+    GroupQ p;
+    const h1 lo = -(z + static_cast<h1>(1024.0f));
+    const h1 hi = -(z + static_cast<h1>(64.0f));
+    p.zlo = h2{lo, lo};
+    p.zhi = h2{hi, hi};
+    p.s = h2{s, s};
+    return p;
+}
+
+// The magic constant 0x64006400 must live in a VGPR for the compiler to fuse the mask and the
+// or into one v_and_or_b32 (a gfx9 VOP3 instruction encodes no 32-bit literal): kernels create
+// it once with magic_reg() and pass it down.
+__device__ __forceinline__ uint32_t magic_reg() {
+    uint32_t m = 0x64006400u;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
+// One word -> its 8 weights (q - z), exact in fp16 (integers -15 .. 15), in k order.
+__device__ __forceinline__ void unpack_qz(uint32_t w, const GroupQ& p, uint32_t magic, h2 (&d)[4]) {
+    const uint32_t w8 = w >> 8;
+    const h2 sixteenth = h2{static_cast<h1>(0.0625f), static_cast<h1>(0.0625f)};
+    d[0] = bitcast<h2>((w & 0x000F000Fu) | magic) + p.zlo;               // k 0, 1
+    d[1] = bitcast<h2>((w & 0x00F000F0u) | magic) * sixteenth + p.zhi;   // k 2, 3
+    d[2] = bitcast<h2>((w8 & 0x000F000Fu) | magic) + p.zlo;              // k 4, 5
+    d[3] = bitcast<h2>((w8 & 0x00F000F0u) | magic) * sixteenth + p.zhi;  // k 6, 7
+}
+
+// One word -> its 8 dequantized weights fp16_rne((q - z) * s) in k order: the exact integer
+// (q - z) times s is a single rounding, so the bits equal fp32 (q - z) * s rounded to fp16.
+__device__ __forceinline__ h8 dequant_word(uint32_t w, const GroupQ& p, uint32_t magic) {
+    h2 d[4];
+    unpack_qz(w, p, magic, d);
+    d[0] *= p.s;
+    d[1] *= p.s;
+    d[2] *= p.s;
+    d[3] *= p.s;
+    return h8{d[0].x, d[0].y, d[1].x, d[1].y, d[2].x, d[2].y, d[3].x, d[3].y};
+}
+
+// Scales and zeros are loaded as raw 16-bit values into 32-bit registers, and only turned into
+// fp16 where they are used: the compiler then has no reason to touch a prefetched value (and
+// wait for its load) before the step that needs it.
+__device__ __forceinline__ uint32_t load_u16(const h1* p) { return *reinterpret_cast<const uint16_t*>(p); }
+__device__ __forceinline__ h1 as_h1(uint32_t v) { return bitcast<h1>(static_cast<uint16_t>(v)); }
+
+__device__ __forceinline__ uint32_t word_of(const u4& v, int i) {  // i constant after unrolling
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ u4 load_stream(const u4* p) {  // weights: read once, do not keep
+    return __builtin_nontemporal_load(p);
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+__device__ __forceinline__ f4 mfma16x16x32(const h8& a, const h8& b, const f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Row of the interleave_gate_up order: destination row n' = 16 T + 8 h + i holds source row
+// h * N/2 + 8 T + i.
+__host__ __device__ __forceinline__ int interleaved_source_row(int nprime, int n) {
+    const int t = nprime >> 4, h = (nprime >> 3) & 1, i = nprime & 7;
+    return h * (n >> 1) + 8 * t + i;
+}
+__host__ __device__ __forceinline__ int interleaved_dest_row(int src, int n) {
+    const int half = n >> 1, h = src >= half ? 1 : 0, rem = src - h * half;
+    return 16 * (rem >> 3) + 8 * h + (rem & 7);
+}
+
+}  // namespace tw4
+
+// ------------------------------------------------------------------------------- host plumbing
+namespace tw4host {
+
+void set_error(const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+
+}  // namespace tw4host
+
+#define TW4_REQUIRE(cond, code, ...)          \
+    do {                                      \
+        if (!(cond)) {                        \
+            tw4host::set_error(__VA_ARGS__);  \
+            return (code);                    \
+        }                                     \
+    } while (0)
+
+#define TW4_LAUNCH_CHECK(what)                                           \
+    do {                                                                 \
+        hipError_t e_ = hipGetLastError();                               \
+        if (e_ != hipSuccess) return tw4host::hip_fail(e_, (what));      \
+    } while (0)

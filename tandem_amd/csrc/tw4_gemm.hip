@@ -1,0 +1,435 @@
+// Fused-dequant GEMM, M > 16 (prefill and batched decode): y[M, N] = x[M, K] @ dequant(W)^T.
+//
+// Workgroup tile: BM = 16 MT tokens x BN = 16 NT WN weight rows. Wavefront (wn, wk) owns the
+// NT row tiles (nblk WN + wn) NT .. + NT - 1 and, of every K step, quant group step WK + wk.
+//   x:       the workgroup's BM x 128 tile of each group goes global -> registers -> LDS, double
+//            buffered (the next step's global loads are in flight while the current step
+//            computes), one barrier per step. All WN wavefronts read it, so LDS carries the reuse.
+//            16-byte chunk c of token row rho is stored at chunk c ^ (rho & 15): the 16 lanes of a
+//            ds_read_b128 (rows rho = 16 b + r, same chunk) then touch 16 different chunks.
+//   weights: each wavefront streams its own (row tile, group) blocks with one non-temporal
+//            global_load_dwordx4 per lane, one step ahead in registers; no other wavefront of
+//            the workgroup reads them, so they skip LDS.
+//   math:    v_mfma_f32_16x16x32_f16, A = dequantized weights fp16_rne((q - z) s) (16 rows x
+//            32 k), B = x (32 k x 16 tokens), the same k permutation as the decode kernels:
+//            lane (kb, r), step s <-> k = 128 g + 32 kb + 8 s .. + 7. D lane (kb, r) = rows
+//            4 kb + i of token r.
+//   WK = 2:  the two K wavefronts add their sums in LDS at the end.
+//   split-K: work units 0 .. dp - 1 are whole tiles; each later tile is shared by `splits` units
+//            that take contiguous ranges of K steps. A unit stores its fp32 partial tile to ws,
+//            then one agent-scope atomic on the tile's counter tells the last arriver, which adds
+//            the `splits` partials in split order (the result does not depend on arrival order),
+//            writes y and returns the counter to zero for the next call.
+//   act = 1: SwiGLU epilogue as in the decode kernel (gate rows 4 kb + i and up rows 8 + 4 kb + i
+//            sit in lanes l and l + 32).
+//   grid:    work units are re-numbered so that each XCD (workgroups are dealt to the 8 XCDs
+//            round-robin) runs a contiguous range; tiles are ordered in bands of 8 token blocks,
+//            token block fastest, so concurrently running workgroups of one XCD share weight
+//            tiles in its L2.
+#include <algorithm>
+#include <type_traits>
+
+#include "tw4_common.h"
+
+namespace tw4 {
+
+template <int MT, int NT, int WN, int WK, int ST>
+struct GemmCfg {
+    static constexpr int BM = 16 * MT;
+    static constexpr int BN = 16 * NT * WN;
+    static constexpr int THREADS = WN * WK * 64;
+    static constexpr int XCH = BM * 16;         // 16-byte chunks of one group's x tile
+    static constexpr int STEP_CH = WK * XCH;    // chunks of one K step
+    static constexpr int XIT = (STEP_CH + THREADS - 1) / THREADS;
+    static constexpr int RING = 2 * STEP_CH * 16;
+    static constexpr int RED = (WK - 1) * WN * NT * MT * 64 * 16;
+    static constexpr int LDS = RING > RED ? RING : RED;
+};
+
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+    if (n < 16) return b;
+    const int q = n >> 3, rr = n & 7, xcd = b & 7, idx = b >> 3;
+    return xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
+}
+
+template <int MT, int NT, int WN, int WK, int ST>
+__global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
+    const h1* __restrict__ x, const u4* __restrict__ w, const h1* __restrict__ scales, const h1* __restrict__ zeros,
+    h1* __restrict__ y, float* __restrict__ ws, int* __restrict__ locks, int M, int N, int K, int mb, int nb, int dp,
+    int splits, int act) {
+    using C = GemmCfg<MT, NT, WN, WK, ST>;
+    extern __shared__ u4 lds[];
+    __shared__ int last_flag;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave % WN, wk = wave / WN;
+    const int r = lane & 15, kb = lane >> 4;
+    const int G = K >> 7, tiles_n = (N + 15) >> 4;
+    const int steps = (G + WK - 1) / WK;
+
+    const int unit = xcd_remap(blockIdx.x, gridDim.x);
+    const bool whole = unit < dp;
+    const int su = unit - dp;
+    const int tile = whole ? unit : dp + su / splits;
+    const int split = whole ? 0 : su % splits;
+    const int nsplit = whole ? 1 : splits;
+    const int step0 = static_cast<int>(static_cast<int64_t>(split) * steps / nsplit);
+    const int nst = static_cast<int>(static_cast<int64_t>(split + 1) * steps / nsplit) - step0;
+    const int band = tile / (8 * nb), band_rows = min(mb - band * 8, 8), rin = tile - band * 8 * nb;
+    const int mblk = band * 8 + rin % band_rows, nblk = rin / band_rows;
+    const int m0 = mblk * C::BM;
+    const int wt0 = (nblk * WN + wn) * NT;
+
+    // x chunks of this thread: source offset (fp16 elements, group 0) and LDS slot offset (u4)
+    int64_t xsrc[C::XIT];
+    int xdst[C::XIT], xgrp[C::XIT];
+#pragma unroll
+    for (int it = 0; it < C::XIT; ++it) {
+        const int c = min(it * C::THREADS + tid, C::STEP_CH - 1);
+        const int u = c / C::XCH, cc = c % C::XCH, rho = cc >> 4, ch = cc & 15;
+        xsrc[it] = static_cast<int64_t>(min(m0 + rho, M - 1)) * K + 8 * ch;
+        xdst[it] = u * C::XCH + rho * 16 + (ch ^ (rho & 15));
+        xgrp[it] = u;
+    }
+    // weight blocks and group parameters of this wavefront's row tiles
+    const u4* wb[NT];
+    int64_t sb[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int tt = min(wt0 + t, tiles_n - 1);
+        wb[t] = w + static_cast<int64_t>(tt) * G * kBlockU4 + lane;
+        sb[t] = static_cast<int64_t>(min(16 * tt + r, N - 1)) * G;  // padding rows: row N - 1's, never stored
+    }
+    const uint32_t magic = magic_reg();
+
+    u4 xr[C::XIT];
+    auto load_x = [&](int step) {
+#pragma unroll
+        for (int it = 0; it < C::XIT; ++it) {
+            const int g = min(step * WK + xgrp[it], G - 1);
+            xr[it] = *reinterpret_cast<const u4*>(x + xsrc[it] + 128 * g);
+        }
+    };
+    auto store_x = [&](int slot) {
+        u4* dst = lds + slot * C::STEP_CH;
+#pragma unroll
+        for (int it = 0; it < C::XIT; ++it)
+            if (C::STEP_CH % C::THREADS == 0 || it * C::THREADS + tid < C::STEP_CH) dst[xdst[it]] = xr[it];
+    };
+    struct WSet {
+        u4 w[NT];
+        uint32_t s[NT], z[NT];
+    };
+    auto load_w = [&](int step, WSet& ws) {
+        const int g = min(step * WK + wk, G - 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            ws.w[t] = load_stream(wb[t] + static_cast<int64_t>(g) * kBlockU4);
+            ws.s[t] = load_u16(scales + sb[t] + g);
+            ws.z[t] = load_u16(zeros + sb[t] + g);
+        }
+    };
+
+    f4 acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One K step: issue the next step's x (then weight) loads, compute this step from LDS and
+    // registers, park the next x tile in the other LDS slot, barrier. x is issued first, so the
+    // wait before store_x does not wait for the weight prefetch.
+    auto step_fn = [&](auto prefetch, int ls, const WSet& cur, WSet& nxt) {
+        constexpr bool more = decltype(prefetch)::value;
+        const int step = step0 + ls;
+        if constexpr (more) {
+            load_x(step + 1);
+            load_w(step + 1, nxt);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math: the scheduler would sink it
+        {  // no branch: a group past G (WK = 2, odd G) gets scale 0
+            const bool valid = step * WK + wk < G;
+            const u4* xs = lds + (ls & 1) * C::STEP_CH + wk * C::XCH;
+            GroupQ p[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                p[t] = group_q(valid ? as_h1(cur.s[t]) : static_cast<h1>(0.0f), as_h1(cur.z[t]));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                h8 xb[MT];
+#pragma unroll
+                for (int b = 0; b < MT; ++b) xb[b] = bitcast<h8>(xs[(16 * b + r) * 16 + ((4 * kb + s) ^ r)]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const h8 a = dequant_word(word_of(cur.w[t], s), p[t], magic);
+#pragma unroll
+                    for (int b = 0; b < MT; ++b) acc[t][b] = mfma16x16x32(a, xb[b], acc[t][b]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (more) store_x((ls + 1) & 1);
+        __syncthreads();
+    };
+    const std::true_type pf;
+    const std::false_type last;
+
+    WSet wa, wb2;
+    load_x(step0);
+    load_w(step0, wa);
+    store_x(0);
+    __syncthreads();
+    // steady state: every step prefetches (no branch around the loads, so the waits stay exact);
+    // the unit's last step prefetches nothing
+    int ls = 0;
+    for (; ls + 2 < nst; ls += 2) {
+        step_fn(pf, ls, wa, wb2);
+        step_fn(pf, ls + 1, wb2, wa);
+    }
+    if (ls + 2 == nst) {
+        step_fn(pf, ls, wa, wb2);
+        step_fn(last, ls + 1, wb2, wa);
+    } else if (ls + 1 == nst) {
+        step_fn(last, ls, wa, wb2);
+    }
+
+    if constexpr (WK > 1) {  // fold the K wavefronts wk > 0 into wk = 0 (the ring is free after the last barrier)
+        f4* red = reinterpret_cast<f4*>(lds);
+        if (wk > 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) red[((((wk - 1) * WN + wn) * NT + t) * MT + b) * 64 + lane] = acc[t][b];
+        }
+        __syncthreads();
+        if (wk == 0) {
+#pragma unroll
+            for (int v = 1; v < WK; ++v)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int b = 0; b < MT; ++b) acc[t][b] += red[((((v - 1) * WN + wn) * NT + t) * MT + b) * 64 + lane];
+        }
+    }
+
+    if (nsplit > 1) {
+        constexpr int V = NT * MT * 64;  // f4 per wavefront partial
+        const int st = tile - dp;        // index among the split tiles
+        f4* wsv = reinterpret_cast<f4*>(ws);
+        if (wk == 0) {
+            f4* mine = wsv + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) mine[(t * MT + b) * 64] = acc[t][b];
+        }
+        __threadfence();  // release: the partial tile is visible device-wide before the count
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = old == splits - 1;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();  // acquire: every split's partial tile is visible
+        if (wk == 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int v = 0; v < splits; ++v) {
+                const f4* other = wsv + ((static_cast<int64_t>(st) * splits + v) * WN + wn) * V + lane;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int b = 0; b < MT; ++b) acc[t][b] += __builtin_nontemporal_load(other + (t * MT + b) * 64);
+            }
+        }
+        if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (wk != 0) return;
+
+    if (act) {  // N % 16 == 0 (checked on the host)
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = wt0 + t;
+#pragma unroll
+            for (int b = 0; b < MT; ++b) {
+                f4 up;
+                up.x = __shfl_xor(acc[t][b].x, 32);
+                up.y = __shfl_xor(acc[t][b].y, 32);
+                up.z = __shfl_xor(acc[t][b].z, 32);
+                up.w = __shfl_xor(acc[t][b].w, 32);
+                const int m = m0 + 16 * b + r;
+                if (kb >= 2 || m >= M || tt >= tiles_n) continue;
+                const f4 g = acc[t][b];
+                const h4 o = h4{static_cast<h1>(silu(g.x) * up.x), static_cast<h1>(silu(g.y) * up.y),
+                                static_cast<h1>(silu(g.z) * up.z), static_cast<h1>(silu(g.w) * up.w)};
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + 8 * tt + 4 * kb) = o;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = 16 * (wt0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+        if (n >= N) continue;
+#pragma unroll
+        for (int b = 0; b < MT; ++b) {
+            const int m = m0 + 16 * b + r;
+            if (m >= M) continue;
+            const f4 a = acc[t][b];
+            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                h4{static_cast<h1>(a.x), static_cast<h1>(a.y), static_cast<h1>(a.z), static_cast<h1>(a.w)};
+        }
+    }
+}
+
+// Compiled GEMM configurations (MT, NT, WN, WK, ST).
+#define TW4_GEMM_CONFIGS(X)                                                                               \
+    X(1, 1, 4, 1, 2) X(1, 2, 4, 1, 2) X(2, 1, 4, 1, 2) X(2, 2, 4, 1, 2) X(2, 1, 4, 2, 2) X(2, 2, 4, 2, 2) \
+    X(4, 1, 4, 1, 2) X(4, 2, 4, 1, 2) X(4, 2, 4, 2, 2) X(4, 4, 4, 1, 2) X(8, 1, 4, 1, 2) X(8, 2, 4, 1, 2) \
+    X(8, 4, 4, 1, 2) X(8, 2, 2, 1, 2) X(4, 4, 2, 1, 2)
+
+constexpr int kMaxDevices = 64;
+#define TW4_COUNT(MT, NT, WN, WK, ST) +1
+constexpr int kGemmConfigs = 0 TW4_GEMM_CONFIGS(TW4_COUNT);
+#undef TW4_COUNT
+
+struct DeviceInfo {
+    int ready;
+    int cus;
+    int occupancy[kGemmConfigs];  // resident workgroups per CU
+};
+static DeviceInfo g_dev[kMaxDevices];
+
+template <int MT, int NT, int WN, int WK, int ST>
+int gemm_prepare(int dev, int index) {
+    using C = GemmCfg<MT, NT, WN, WK, ST>;
+    auto kern = gemm_kernel<MT, NT, WN, WK, ST>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "init: hipFuncSetAttribute");
+    int per_cu = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, C::THREADS, C::LDS);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "init: hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    g_dev[dev].occupancy[index] = per_cu > 0 ? per_cu : 1;
+    return TW4_OK;
+}
+
+thread_local int g_last_blocks = 0, g_last_dp = 0, g_last_splits = 0;
+
+template <int MT, int NT, int WN, int WK, int ST>
+int gemm_launch(int dev, int index, const h1* x, const u4* w, const h1* s, const h1* z, h1* y, float* ws,
+                int* locks, int64_t ws_floats, int64_t n_locks, int M, int N, int K, int splits, int act,
+                hipStream_t stream) {
+    using C = GemmCfg<MT, NT, WN, WK, ST>;
+    const int G = K >> 7, steps = (G + WK - 1) / WK;
+    const int mb = (M + C::BM - 1) / C::BM, tiles_n = (N + 15) >> 4;
+    const int nb = (tiles_n * 16 + C::BN - 1) / C::BN;
+    const int64_t tiles64 = static_cast<int64_t>(mb) * nb;
+    TW4_REQUIRE(tiles64 < (1LL << 30), TW4_EINVAL, "gemm: too many tiles (%lld)", static_cast<long long>(tiles64));
+    const int tiles = static_cast<int>(tiles64);
+    const int64_t tile_floats = static_cast<int64_t>(C::BM) * C::BN;
+    int dp = tiles, sp = 1;
+    if (splits == 0) {  // whole tiles for the full waves; split the last, partial wave along K
+        const int slots = g_dev[dev].occupancy[index] * g_dev[dev].cus;
+        const int rem = tiles % slots;
+        double best = 1.0;  // s = 1: one more wave of whole tiles, in units of one tile's time
+        for (int c = 2; c <= 8 && c <= steps && rem > 0; ++c) {
+            if (static_cast<int64_t>(rem) * c * tile_floats > ws_floats || rem > n_locks) break;
+            // the split wave's time in tile units, plus a fix-up cost per extra split
+            const double t = static_cast<double>((static_cast<int64_t>(rem) * c + slots - 1) / slots) / c + 0.02 * c;
+            if (t < best) best = t, sp = c;
+        }
+        if (sp > 1) dp = tiles - rem;
+    } else if (splits > 1) {
+        TW4_REQUIRE(splits <= steps, TW4_EINVAL, "gemm: splits %d > K steps %d", splits, steps);
+        TW4_REQUIRE(static_cast<int64_t>(tiles) * splits * tile_floats <= ws_floats && tiles <= n_locks, TW4_ESPACE,
+                    "gemm: split-K workspace too small for %d tiles x %d splits", tiles, splits);
+        dp = 0, sp = splits;
+    }
+    const int64_t blocks = dp + static_cast<int64_t>(tiles - dp) * sp;
+    TW4_REQUIRE(blocks < (1LL << 31), TW4_EINVAL, "gemm: grid too large");
+    g_last_blocks = static_cast<int>(blocks), g_last_dp = dp, g_last_splits = sp;
+    gemm_kernel<MT, NT, WN, WK, ST><<<static_cast<unsigned>(blocks), C::THREADS, C::LDS, stream>>>(
+        x, w, s, z, y, ws, locks, M, N, K, mb, nb, dp, sp, act);
+    TW4_LAUNCH_CHECK("gemm: launch");
+    return TW4_OK;
+}
+
+int device_prepare(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        tw4host::set_error("init: device %d out of range", dev);
+        return TW4_EINVAL;
+    }
+    if (g_dev[dev].ready) return TW4_OK;
+    int cus = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "init: multiprocessor count");
+    g_dev[dev].cus = cus;
+    int index = 0, rc = TW4_OK;
+#define TW4_PREP(MT, NT, WN, WK, ST) \
+    if (rc == TW4_OK) rc = gemm_prepare<MT, NT, WN, WK, ST>(dev, index); \
+    ++index;
+    TW4_GEMM_CONFIGS(TW4_PREP)
+#undef TW4_PREP
+    if (rc == TW4_OK) g_dev[dev].ready = 1;
+    return rc;
+}
+
+}  // namespace tw4
+
+using namespace tw4;
+
+int tw4_gemm_prepare_device(int dev) { return device_prepare(dev); }
+
+extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                        uint16_t* y, float* ws, int32_t* locks, int64_t ws_floats, int64_t n_locks, int M, int N,
+                        int K, int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
+                        void* stream) {
+    TW4_REQUIRE(x && packed && scales && zeros && y, TW4_EINVAL, "gemm: null pointer");
+    TW4_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, TW4_EINVAL, "gemm: x must be 16-byte aligned");
+    TW4_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 16 == 0, TW4_EINVAL, "gemm: packed must be 16-byte aligned");
+    TW4_REQUIRE(reinterpret_cast<uintptr_t>(y) % 8 == 0, TW4_EINVAL, "gemm: y must be 8-byte aligned");
+    TW4_REQUIRE(K > 0 && K % 128 == 0, TW4_EINVAL, "gemm: K %% 128 == 0 (K = %d)", K);
+    TW4_REQUIRE(N > 0 && N % 8 == 0, TW4_EINVAL, "gemm: N %% 8 == 0 (N = %d)", N);
+    TW4_REQUIRE(M >= 0, TW4_EINVAL, "gemm: M >= 0 (M = %d)", M);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "gemm: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    TW4_REQUIRE(splits >= 0 && splits <= 16, TW4_EINVAL, "gemm: splits 0 (split the last wave) or 1 .. 16");
+    TW4_REQUIRE(splits <= 1 || (ws && locks), TW4_EINVAL, "gemm: split-K needs a workspace and counters");
+    if (M == 0) return TW4_OK;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "gemm: hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices || !g_dev[dev].ready) {
+        int rc = device_prepare(dev);
+        if (rc) return rc;
+    }
+    if (splits == 0 && !(ws && locks)) splits = 1;
+    auto xp = reinterpret_cast<const h1*>(x);
+    auto wp = reinterpret_cast<const u4*>(packed);
+    auto sp = reinterpret_cast<const h1*>(scales);
+    auto zp = reinterpret_cast<const h1*>(zeros);
+    auto yp = reinterpret_cast<h1*>(y);
+    auto st = static_cast<hipStream_t>(stream);
+    int index = 0;
+#define TW4_GEMM_CASE(MT, NT, WN, WK, ST)                                                                        \
+    if (mt == MT && nt == NT && warps_n == WN && warps_k == WK && stages == ST)                                  \
+        return gemm_launch<MT, NT, WN, WK, ST>(dev, index, xp, wp, sp, zp, yp, ws, locks, ws_floats, n_locks, M, \
+                                               N, K, splits, act, st);                                           \
+    ++index;
+    TW4_GEMM_CONFIGS(TW4_GEMM_CASE)
+#undef TW4_GEMM_CASE
+    tw4host::set_error("gemm: unsupported mt / nt / warps_n / warps_k / stages %d / %d / %d / %d / %d", mt, nt,
+                       warps_n, warps_k, stages);
+    return TW4_ECONFIG;
+}
+
+extern "C" int tw4_gemm_last_grid(int* blocks, int* dp_tiles, int* splits) {
+    if (blocks) *blocks = g_last_blocks;
+    if (dp_tiles) *dp_tiles = g_last_dp;
+    if (splits) *splits = g_last_splits;
+    return TW4_OK;
+}

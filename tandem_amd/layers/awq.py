@@ -1,0 +1,242 @@
+"""4-bit AWQ weights (W4A16) on MI355X: load-time repack, decode kernels, prefill path.
+
+Drop-in for python/tandem/layers/awq.py (12vivi/tandem): the same AutoAWQ "gemm" buffers, the same
+W4Linear constructor / ``enable_silu_mul`` / ``finalize`` / ``forward`` contract, the same per-GPU
+config tables and ``TANDEM_W4_GEMM`` switch. The kernels are hand-written HIP for gfx950
+(libtandem_w4.so, include/tandem_w4.h); there is no Triton and no CPU path.
+
+AutoAWQ "gemm" checkpoints store each linear layer as
+    qweight [K, N/8] int32   8 4-bit weights per int32 along the output dim, AWQ nibble order
+    qzeros  [K/G, N/8] int32 zero points, packed the same way
+    scales  [K/G, N]         one scale per group of G = 128 inputs
+and w[k, n] = (q[k, n] - z[k // G, n]) * s[k // G, n].
+
+``finalize`` repacks once, on the GPU, into the tile layout of the MI355X kernels:
+    packed [Npad, K/8] int32  (Npad = N rounded up to 16), viewed as [Npad/16][K/128][4 kb][16 r][4 s]:
+           word (kb, r, s) of row tile T and group g holds the 8 consecutive weights
+           k = 128 g + 32 kb + 8 s + 2 q + e (q = 0..3, e = 0..1) of row 16 T + r in nibble q + 4 e;
+           one (row tile, group) block is 1 KB, read by one 64-lane wavefront with one 16-byte
+           load per lane (lane 16 kb + r). Rows >= N are zero.
+    scales [N, K/G] float16, zeros [N, K/G] float16 (the integer zero point, exact)
+The nibble order inside a word is the reference's (python/tandem/layers/awq.py:12-20); the word
+order is this build's (the reference keeps each row contiguous: [N][K/G][4 j][4 cc]).
+
+Kernels (libtandem_w4.so): w4_gemv (M <= 4, vector ALUs), w4_mma (M <= 16, matrix cores) and
+w4_gemm (M > 16, matrix cores, LDS-staged activations, split-K). Where the table says so, with
+TANDEM_W4_GEMM=0, with TANDEM_NO_CUDA_EXT=1 or for an unaligned x: HIP dequantize to float16 +
+torch.matmul (hipBLASLt).
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from tandem_amd.layers import w4_hip
+
+# AWQ packs output columns j = 0..7 of an int32 in nibble order [0, 2, 4, 6, 1, 3, 5, 7]: column j
+# lives in nibble REVERSE[j] (python/tandem/layers/awq.py:38-39)
+AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
+
+
+def unpack_awq(packed: torch.Tensor) -> torch.Tensor:
+    """[R, C] int32 in AWQ order -> [R, 8 C] int32 values 0..15 (column c*8 + j); a layout utility
+    on any device (python/tandem/layers/awq.py:42-46)."""
+    shifts = torch.tensor([4 * i for i in AWQ_REVERSE_ORDER], dtype=torch.int32, device=packed.device)
+    return ((packed[:, :, None] >> shifts) & 0xF).reshape(packed.shape[0], -1)
+
+
+def pack_rows(q: torch.Tensor) -> torch.Tensor:
+    """[N, K] values 0..15 -> tile layout [Npad, K/8] int32 (see the module docstring); a layout
+    utility on any device. The counterpart of python/tandem/layers/awq.py:49-57 for this build's
+    layout; finalize uses the tw4_repack_awq kernel instead."""
+    n, k = q.shape
+    npad = w4_hip.padded_rows(n)
+    v = torch.zeros((npad, k), dtype=torch.int64, device=q.device)
+    v[:n] = q.to(torch.int64)
+    v = v.view(npad // 16, 16, k // 128, 4, 4, 4, 2)  # [T, r, g, kb, s, q, e]: k = 128 g + 32 kb + 8 s + 2 q + e
+    v = v.permute(0, 2, 3, 1, 4, 5, 6)  # -> [T, g, kb, r, s, q, e]
+    shifts = 4 * (torch.arange(4, device=q.device)[:, None] + 4 * torch.arange(2, device=q.device)[None, :])
+    words = (v << shifts).sum(dim=(-1, -2))  # nibbles do not overlap: sum == or
+    words = torch.where(words >= 1 << 31, words - (1 << 32), words)  # int32 bit pattern
+    return words.reshape(npad, k // 8).to(torch.int32)
+
+
+def repack_awq(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group: int,
+               dtype: torch.dtype = torch.float16, interleave: bool = False
+               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """AWQ (qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N]) -> tile layout (packed [Npad, K/8]
+    int32, scales [N, K/G], zeros [N, K/G]) on the GPU (python/tandem/layers/awq.py:60-68).
+    ``interleave``: rows in interleave_gate_up order (the reference applies interleave_gate_up to
+    the repacked rows, awq.py:237-238; the tile layout takes it inside the repack kernel)."""
+    if group != 128 or qweight.shape[0] % 128 or scales.shape != (qweight.shape[0] // group, 8 * qweight.shape[1]):
+        raise ValueError(f"repack_awq: qweight {tuple(qweight.shape)} scales {tuple(scales.shape)} group {group}")
+    if dtype != torch.float16:
+        raise ValueError("repack_awq: the MI355X kernels take float16 scales and zeros")
+    return w4_hip.repack(qweight, qzeros, scales, interleave=interleave)
+
+
+def interleave_gate_up(t: torch.Tensor) -> torch.Tensor:
+    """Rows [gate (I); up (I)] -> tiles of 16 rows [gate 8i .. 8i+7, up 8i .. 8i+7], the order in
+    which the matrix-core kernels' SwiGLU epilogue finds gate and up of a feature in lanes l and
+    l + 32 (python/tandem/layers/awq.py:71-75). For row-major tensors (scales, zeros, dense
+    weights); the tile-layout `packed` is interleaved by repack_awq(..., interleave=True)."""
+    n = t.shape[0]
+    return t.view(2, n // 16, 8, *t.shape[1:]).transpose(0, 1).reshape(t.shape)
+
+
+def silu_and_mul(y: torch.Tensor) -> torch.Tensor:
+    """[M, 2I] = [gate | up] -> silu(gate) * up (python/tandem/layers/awq.py:78-86, torch branch)."""
+    gate, up = y.chunk(2, dim=-1)
+    return F.silu(gate) * up
+
+
+def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, group: int = 128,
+               dtype: torch.dtype = torch.float16, block_n: int = 32, deinterleave: bool = False) -> torch.Tensor:
+    """-> dense [N, K] (nn.Linear layout), bit-exact fp16_rne((q - z) s), by the HIP dequant kernel
+    (python/tandem/layers/awq.py:122-133). ``deinterleave``: undo interleave_gate_up on the rows.
+    ``block_n`` is accepted for signature compatibility and ignored."""
+    if group != 128:
+        raise ValueError("w4_dequant: group 128 only")
+    if deinterleave and scales.shape[0] % 16:
+        raise ValueError("w4_dequant: deinterleave needs N a multiple of 16")
+    w = w4_hip.dequant(packed, scales, zeros, deinterleave=deinterleave)
+    return w if dtype == torch.float16 else w.to(dtype)
+
+
+# Decode kernel per GPU and (N, K, M), the fastest of bench_w4.py-style sweeps on the GPU:
+#   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4
+#   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 16
+# warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
+# iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
+# (Same dispatch structure as python/tandem/layers/awq.py:136-160.)
+W4Kernel = tuple
+DEFAULT_KERNEL: W4Kernel = ("mma", 4, 2, 1)
+MI355X = "AMD Instinct MI355X"
+W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
+    MI355X: {},
+}
+
+# GEMM for M > 16 per GPU and (N, K) / (N, K, "silu"): ((m_max, config), ...) by increasing m_max;
+# M past the last m_max uses the last entry. config = (MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS) of
+# w4_gemm (BM = 16 MT tokens, each wavefront 16 NT rows, WARPS_N x WARPS_K wavefronts, STAGES-deep
+# LDS ring, SPLITS: split-K of every tile, or 0: of the last, partial wave of tiles only), or None:
+# dequantize to float16 + torch.matmul. Shapes without an entry use DEFAULT_GEMM.
+# TANDEM_W4_GEMM=0: always dequantize + torch.matmul (python/tandem/layers/awq.py:163-186).
+W4Gemm = tuple
+DEFAULT_GEMM: tuple[tuple[int, W4Gemm | None], ...] = (
+    (32, (2, 1, 4, 1, 2, 0)), (64, (4, 1, 4, 1, 2, 0)), (1 << 30, (8, 2, 4, 1, 2, 0)))
+W4_GEMM_KERNELS: dict[str, dict[tuple, tuple[tuple[int, W4Gemm | None], ...]]] = {
+    MI355X: {},
+}
+FUSED_GEMM = os.environ.get("TANDEM_W4_GEMM", "1") != "0"
+
+
+def pick_gemm(table: tuple[tuple[int, W4Gemm | None], ...], m: int) -> W4Gemm | None:
+    """First entry whose m_max >= m, else the last one (python/tandem/layers/awq.py:189-193)."""
+    for m_max, cfg in table:
+        if m <= m_max:
+            return cfg
+    return table[-1][1]
+
+
+def _aligned(x: torch.Tensor) -> bool:
+    return x.dim() == 2 and x.dtype == torch.float16 and x.is_contiguous() and x.data_ptr() % 16 == 0
+
+
+def _hip_ok(x: torch.Tensor) -> bool:
+    """Decode kernels (python/tandem/layers/awq.py:196-198), plus: on a GPU."""
+    return x.is_cuda and _aligned(x) and 1 <= x.shape[0] <= 16
+
+
+def _gemm_ok(x: torch.Tensor) -> bool:
+    """The M > 16 GEMM (python/tandem/layers/awq.py:201-203)."""
+    return FUSED_GEMM and x.is_cuda and _aligned(x) and x.shape[0] > 16
+
+
+class W4Linear(nn.Module):
+    """Linear layer with AWQ 4-bit weights (no bias). Built with the checkpoint's AWQ tensors as
+    buffers (qweight / qzeros / scales, filled by the loader, fused along the output dimension for
+    qkv / gate_up); ``finalize`` repacks them on the GPU into the tile layout
+    (python/tandem/layers/awq.py:206-286).
+
+    ``enable_silu_mul`` (gate_up of a SwiGLU MLP, before ``finalize``): the layer returns
+    silu(gate) * up, [M, out_features / 2], instead of [gate | up]; the matrix-core kernels apply
+    it in their epilogue (rows reordered as interleave_gate_up)."""
+
+    def __init__(self, in_features: int, out_features: int, group: int) -> None:
+        super().__init__()
+        if group != 128 or in_features % group or out_features % 8:
+            raise ValueError(f"W4Linear: {in_features} x {out_features} with group {group} (group 128 only)")
+        self.in_features, self.out_features, self.group = in_features, out_features, group
+        self.awq_layout = True
+        self.silu_mul = False
+        self.register_buffer("qweight", torch.empty(in_features, out_features // 8, dtype=torch.int32))
+        self.register_buffer("qzeros", torch.empty(in_features // group, out_features // 8, dtype=torch.int32))
+        self.register_buffer("scales", torch.empty(in_features // group, out_features, dtype=torch.float16))
+        self.kernels: dict[tuple, W4Kernel] = {}
+        self.gemm_kernels: dict[tuple, tuple[tuple[int, W4Gemm | None], ...]] = {}
+
+    def enable_silu_mul(self) -> bool:
+        if not self.awq_layout or self.out_features % 16:
+            return False
+        self.silu_mul = True
+        return True
+
+    @torch.no_grad()
+    def finalize(self, device_name: str | None = None) -> None:
+        packed, scales, zeros = repack_awq(self.qweight, self.qzeros, self.scales, self.group, torch.float16,
+                                           interleave=self.silu_mul)
+        del self._buffers["qweight"], self._buffers["qzeros"]
+        self.register_buffer("packed", packed)
+        self.register_buffer("scales", scales)
+        self.register_buffer("zeros", zeros)
+        self.awq_layout = False
+        self.kernels = W4_KERNELS.get(device_name, {}) if device_name else {}
+        self.gemm_kernels = W4_GEMM_KERNELS.get(device_name, {}) if device_name else {}
+        # device set-up and the split-K workspace now, not inside graph capture
+        if w4_hip.load() is not None:
+            w4_hip.workspace(packed.device)
+
+    def _dense(self, x: torch.Tensor) -> torch.Tensor:
+        """HIP dequantize (gate_up: back in [gate | up] row order) + torch.matmul, and the same
+        activation as the unfused path (python/tandem/layers/awq.py:282-286)."""
+        if not x.is_cuda:
+            raise RuntimeError("W4Linear: x must be on the GPU (there is no CPU path)")
+        w = w4_dequant(self.packed, self.scales, self.zeros, self.group, x.dtype, deinterleave=self.silu_mul)
+        y = F.linear(x, w)
+        return silu_and_mul(y) if self.silu_mul else y
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.awq_layout:
+            raise RuntimeError("W4Linear: call finalize() (after moving the layer to the GPU) before forward")
+        if x.dim() == 2 and x.shape[0] == 0:
+            return x.new_empty((0, self.out_features // 2 if self.silu_mul else self.out_features))
+        if _hip_ok(x):
+            ext = w4_hip.load()
+            if ext is not None:
+                m = x.shape[0]
+                key = (self.out_features, self.in_features, m)
+                if self.silu_mul:  # matrix-core kernel only (the epilogue pairs lanes l and l + 32)
+                    kind, *cfg = self.kernels.get((*key, "silu")) or self.kernels.get(key, DEFAULT_KERNEL)
+                    if kind != "mma":
+                        _, *cfg = DEFAULT_KERNEL
+                    return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, 1)
+                kind, *cfg = self.kernels.get(key, DEFAULT_KERNEL)
+                if kind == "gemv" and m <= 4:
+                    return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg)
+                if kind != "mma":
+                    _, *cfg = DEFAULT_KERNEL
+                return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, 0)
+        elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul
+            ext = w4_hip.load()
+            if ext is not None:
+                key = (self.out_features, self.in_features) + (("silu",) if self.silu_mul else ())
+                cfg = pick_gemm(self.gemm_kernels.get(key, DEFAULT_GEMM), x.shape[0])
+                if cfg is not None:
+                    buf, locks = w4_hip.workspace(x.device)
+                    return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
+        return self._dense(x)

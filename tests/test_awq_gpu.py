@@ -1,0 +1,321 @@
+"""GPU parity of the MI355X W4A16 path against the CPU oracle (oracle/awq_oracle.py).
+
+Mirrors tests/test_awq.py of 12vivi/tandem: repack and dequantization (bit-exact here), the row
+interleave, every compiled configuration of the three kernels against the dequantize-then-matmul
+reference, SwiGLU epilogues, split-K counters and graph replay, and the W4Linear layer. Inputs
+follow the reference tests' recipe (q, z uniform in 0..15, s = U[0, 1) * 0.02 + 0.001, x ~ N(0, 1))
+on numpy's seeded generator. Tolerances are the reference's (atol / rtol): 0.05 / 0.02 for the
+vector-ALU GEMV and the layer, 0.02 / 0.01 for the matrix-core kernels, 0.03 / 0.02 (layer) and
+0.02 / 0.01 (kernels) for SwiGLU; every comparison also reports max |err| / max |ref| and the
+cosine similarity, and requires cosine >= 0.9999.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as o
+from tandem_amd.layers import awq, w4_hip
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+SHAPES = ((128, 24), (256, 520), (1024, 64), (4096, 1000))  # (K, N); N % 16 != 0 exercises the padded tile
+DECODE_CONFIGS = ((1, 2, 1), (1, 4, 1), (2, 2, 1), (2, 4, 1), (4, 1, 1), (4, 2, 1), (4, 4, 1), (8, 1, 1), (8, 2, 1),
+                  (2, 2, 2), (4, 1, 2), (4, 2, 2), (8, 1, 2), (8, 2, 2), (4, 4, 2), (2, 4, 2), (16, 1, 1),
+                  (16, 2, 1))  # (warps_k, unroll, ntile)
+GEMM_CONFIGS = ((1, 1, 4, 1, 2), (1, 2, 4, 1, 2), (2, 1, 4, 1, 2), (2, 2, 4, 1, 2), (2, 1, 4, 2, 2), (2, 2, 4, 2, 2),
+                (4, 1, 4, 1, 2), (4, 2, 4, 1, 2), (4, 2, 4, 2, 2), (4, 4, 4, 1, 2), (8, 1, 4, 1, 2), (8, 2, 4, 1, 2),
+                (8, 4, 4, 1, 2), (8, 2, 2, 1, 2), (4, 4, 2, 1, 2))  # (MT, NT, WARPS_N, WARPS_K, STAGES)
+
+
+@pytest.fixture(scope="module")
+def ext():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    e = w4_hip.load()
+    assert e is not None, "TANDEM_NO_CUDA_EXT=1 is set"
+    return e
+
+
+def gpu(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+class Case:
+    """One random AWQ weight on CPU (oracle) and GPU (tile layout)."""
+
+    def __init__(self, k: int, n: int, seed: int, interleave: bool = False):
+        self.k, self.n = k, n
+        self.qweight, self.qzeros, self.scales, self.q, self.z = o.random_awq(k, n, seed=seed)
+        self.w_exact = o.dequant_exact(self.qweight, self.qzeros, self.scales)  # [N, K] float32
+        self.w16 = self.w_exact.astype(np.float16)
+        self.packed, self.s, self.zz = w4_hip.repack(gpu(self.qweight), gpu(self.qzeros), gpu(self.scales),
+                                                     interleave=interleave)
+
+    def x(self, m: int, seed: int) -> np.ndarray:
+        return np.random.default_rng(seed).standard_normal((m, self.k)).astype(np.float16)
+
+
+def check_close(y: torch.Tensor, ref: np.ndarray, atol: float, rtol: float, what) -> None:
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    err = np.abs(got - ref)
+    bad = err > atol + rtol * np.abs(ref)
+    max_rel = float(err.max() / max(np.abs(ref).max(), 1e-6))
+    denom = np.linalg.norm(got) * np.linalg.norm(ref)
+    cos = float((got * ref).sum() / denom) if denom > 0 else 1.0
+    assert not bad.any(), (what, f"max|err| {err.max():.4g}", f"max_rel {max_rel:.3g}", f"cos {cos:.7f}")
+    assert cos >= 0.9999 or np.abs(ref).max() < 1e-3, (what, cos)
+
+
+# ------------------------------------------------------------------ repack and dequantization
+@pytest.mark.parametrize("k,n", [(256, 64), (1024, 384), (4096, 1024), (128, 24), (256, 520), (4096, 1000)])
+def test_repack_and_dequant_bit_exact(k, n):
+    """HIP repack + HIP dequant == oracle fp16_rne((q - z) s), every bit (tests/test_awq.py:41-47
+    checks atol 1e-3; here the bar is equality)."""
+    c = Case(k, n, seed=k + n)
+    assert c.packed.shape == (w4_hip.padded_rows(n), k // 8) and c.s.shape == (n, k // 128)
+    assert torch.equal(c.s.cpu(), torch.from_numpy(c.scales.T.copy()))
+    assert torch.equal(c.zz.cpu(), torch.from_numpy(c.z.T.astype(np.float16).copy()))
+    assert torch.equal(c.packed.cpu(), awq.pack_rows(torch.from_numpy(c.q.T.copy())))
+    w = awq.w4_dequant(c.packed, c.s, c.zz)
+    assert w.shape == (n, k)
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), o.dequant(c.qweight, c.qzeros, c.scales).view(np.uint16))
+
+
+def test_dequant_full_size_gate_up_bit_exact():
+    """Qwen3-8B gate_up (K 4096, N 24576): the whole 201 MB fp16 weight, bit for bit."""
+    c = Case(4096, 24576, seed=77)
+    w = awq.w4_dequant(c.packed, c.s, c.zz).cpu().numpy()
+    assert np.array_equal(w.view(np.uint16), c.w16.view(np.uint16))
+
+
+def test_dequant_deinterleave():
+    """Interleaved repack + de-interleaving dequant == plain dequant (tests/test_awq.py:50-55), and the
+    interleaved tile layout holds interleave_gate_up's row order."""
+    c = Case(256, 96, seed=7)
+    pi, si, zi = w4_hip.repack(gpu(c.qweight), gpu(c.qzeros), gpu(c.scales), interleave=True)
+    assert torch.equal(awq.w4_dequant(pi, si, zi, deinterleave=True), awq.w4_dequant(c.packed, c.s, c.zz))
+    assert torch.equal(si, awq.interleave_gate_up(c.s))
+    q_rows = torch.from_numpy(o.interleave_gate_up(c.q.T.copy()))
+    assert torch.equal(pi.cpu(), awq.pack_rows(q_rows))
+
+
+# ----------------------------------------------------------------------- per-kernel parity
+def test_gemv_every_config(ext):
+    """Vector-ALU kernel vs the dequantized matmul, M = 1..4, every compiled config
+    (tests/test_awq.py:203-214)."""
+    for k, n in SHAPES:
+        c = Case(k, n, seed=3)
+        for m in range(1, 5):
+            x = c.x(m, seed=100 + m)
+            ref = o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                check_close(ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg))
+
+
+def test_mma_every_config(ext):
+    """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229)."""
+    for k, n in SHAPES:
+        c = Case(k, n, seed=4)
+        for m in range(1, 17):
+            x = c.x(m, seed=200 + m)
+            ref = o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg))
+
+
+def test_mma_silu_mul(ext):
+    """SwiGLU epilogue (act = 1) on interleaved rows: y = silu(gate) * up (tests/test_awq.py:302-314)."""
+    for k, n in ((128, 32), (1024, 512), (4096, 1024)):
+        c = Case(k, n, seed=6, interleave=True)
+        for m in range(1, 17):
+            x = c.x(m, seed=300 + m)
+            ref = o.swiglu_reference(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
+                assert y.shape == (m, n // 2)
+                check_close(y, ref, 0.02, 0.01, (k, n, m, cfg))
+
+
+def test_gemm_every_config(ext):
+    """M > 16 GEMM: every compiled config, partial token and row tiles, split-K of every tile or of
+    the last wave only; the counters are back at zero after each call (tests/test_awq.py:232-259)."""
+    buf, locks = w4_hip.workspace(DEV)
+    for k, n in SHAPES:
+        c = Case(k, n, seed=7)
+        for m in (17, 40, 64, 130):
+            x = c.x(m, seed=400 + m)
+            ref = o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in GEMM_CONFIGS:
+                for splits in (0, 1, 3):
+                    if splits > (k // 128 + cfg[3] - 1) // cfg[3]:
+                        continue
+                    y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 0)
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
+    torch.cuda.synchronize()
+    assert int(locks.abs().sum()) == 0
+
+
+def test_gemm_silu_mul(ext):
+    """The GEMM's SwiGLU epilogue (act = 1): [M, N / 2] (tests/test_awq.py:262-276)."""
+    buf, locks = w4_hip.workspace(DEV)
+    for k, n in ((128, 32), (1024, 512), (4096, 1024)):
+        c = Case(k, n, seed=8, interleave=True)
+        for m in (17, 64, 100):
+            x = c.x(m, seed=500 + m)
+            ref = o.swiglu_reference(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in GEMM_CONFIGS:
+                for splits in (0, 1, 2):
+                    if splits > (k // 128 + cfg[3] - 1) // cfg[3]:
+                        continue
+                    y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 1)
+                    assert y.shape == (m, n // 2)
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
+    torch.cuda.synchronize()
+    assert int(locks.abs().sum()) == 0
+
+
+def test_gemm_split_k_deterministic(ext):
+    """The last arriver adds the splits in split order: identical bits on every call."""
+    buf, locks = w4_hip.workspace(DEV)
+    c = Case(4096, 1024, seed=9)
+    xg = gpu(c.x(33, seed=9))
+    first = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, 2, 1, 4, 1, 2, 8, 0)
+    for _ in range(5):
+        assert torch.equal(ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, 2, 1, 4, 1, 2, 8, 0), first)
+
+
+def test_gemm_split_k_graph_replay(ext):
+    """Split-K inside a HIP graph: the counters are reset by the kernel, so replays stay correct
+    (tests/test_awq.py:279-299)."""
+    buf, locks = w4_hip.workspace(DEV)
+    c = Case(1024, 512, seed=9)
+    x = gpu(c.x(33, seed=10))
+    cfg = (2, 2, 4, 2, 2, 4, 0)
+    ext.w4_gemm(x, c.packed, c.s, c.zz, buf, locks, *cfg)  # first launch outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = ext.w4_gemm(x, c.packed, c.s, c.zz, buf, locks, *cfg)
+    rng = np.random.default_rng(11)
+    for _ in range(3):
+        xn = rng.standard_normal((33, 1024)).astype(np.float16)
+        x.copy_(gpu(xn))
+        graph.replay()
+        torch.cuda.synchronize()
+        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "replay")
+    assert int(locks.abs().sum()) == 0
+
+
+def test_decode_graph_replay(ext):
+    """The decode kernels under graph capture and replay, eager work in between."""
+    c = Case(4096, 1024, seed=12)
+    x = gpu(c.x(4, seed=12))
+    ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
+    ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y1 = ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
+        y2 = ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
+    rng = np.random.default_rng(13)
+    for _ in range(3):
+        xn = rng.standard_normal((4, 4096)).astype(np.float16)
+        x.copy_(gpu(xn))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = o.linear(xn, c.w_exact)
+        check_close(y1, ref, 0.02, 0.01, "mma replay")
+        check_close(y2, ref, 0.05, 0.02, "gemv replay")
+
+
+# ----------------------------------------------------------------- full Qwen3-8B shapes
+QWEN3_8B = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+SEEDS = {"qkv": 31, "o": 32, "gate_up": 33, "down": 34}
+
+
+@pytest.mark.parametrize("proj", list(QWEN3_8B))
+def test_qwen3_8b_shapes(ext, proj):
+    """Every kernel at the real shape vs the oracle's dequantize-then-matmul (float64)."""
+    k, n = QWEN3_8B[proj]
+    c = Case(k, n, seed=SEEDS[proj])
+    buf, locks = w4_hip.workspace(DEV)
+    for m in (1, 4):
+        x = c.x(m, seed=m)
+        check_close(ext.w4_gemv(gpu(x), c.packed, c.s, c.zz, 4, 2, 1), o.linear(x, c.w_exact), 0.05, 0.02, (proj, m))
+    for m in (1, 8, 16):
+        x = c.x(m, seed=m)
+        check_close(ext.w4_mma(gpu(x), c.packed, c.s, c.zz, 4, 2, 1, 0), o.linear(x, c.w_exact), 0.02, 0.01,
+                    (proj, m))
+    for m, cfg in ((32, (2, 1, 4, 1, 2, 0)), (64, (4, 1, 4, 1, 2, 0)), (256, (8, 2, 4, 1, 2, 0))):
+        x = c.x(m, seed=m)
+        check_close(ext.w4_gemm(gpu(x), c.packed, c.s, c.zz, buf, locks, *cfg, 0), o.linear(x, c.w_exact), 0.02,
+                    0.01, (proj, m, cfg))
+
+
+# --------------------------------------------------------------------------- W4Linear layer
+def _layer(k, n, seed, silu_mul=False):
+    c = Case(k, n, seed=seed)
+    layer = awq.W4Linear(k, n, 128).to(DEV)
+    layer.qweight.copy_(gpu(c.qweight))
+    layer.qzeros.copy_(gpu(c.qzeros))
+    layer.scales.copy_(gpu(c.scales))
+    if silu_mul:
+        assert layer.enable_silu_mul()
+    layer.finalize(torch.cuda.get_device_name())
+    return layer, c
+
+
+def test_w4linear_small_and_large_batch():
+    """tests/test_awq.py:87-103: decode kernels for M <= 16, the GEMM above, the unaligned-x
+    fallback, and table entries (a GEMM config with split-K, or None = dequantize + matmul)."""
+    k, n = 512, 256
+    layer, c = _layer(k, n, seed=2)
+    assert not layer.awq_layout and not hasattr(layer, "qweight") and layer.packed.shape == (n, k // 8)
+    rng = np.random.default_rng(20)
+    for m in (1, 3, 8, 12, 16, 37, 300):
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, m)
+    for m in (3, 40):  # not 16-byte aligned: dequantize + matmul
+        xu = torch.empty(m * k + 1, device=DEV, dtype=torch.float16)[1:].view(m, k)
+        xn = rng.standard_normal((m, k)).astype(np.float16)
+        xu.copy_(gpu(xn))
+        check_close(layer(xu), o.linear(xn, c.w_exact), 0.05, 0.02, ("unaligned", m))
+    for cfg in ((2, 2, 4, 2, 2, 2), (4, 2, 4, 1, 2, 0), None):
+        layer.gemm_kernels = {(n, k): ((1 << 30, cfg),)}
+        x = rng.standard_normal((50, k)).astype(np.float16)
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, cfg)
+    assert layer(torch.empty(0, k, device=DEV, dtype=torch.float16)).shape == (0, n)
+
+
+def test_w4linear_silu_mul():
+    """tests/test_awq.py:106-118: gate_up with SwiGLU, rows interleaved at finalize; the epilogue in
+    the decode kernels (M <= 16) and the GEMM (M > 16); dequantize + matmul for unaligned inputs."""
+    k, n = 512, 384
+    layer, c = _layer(k, n, seed=5, silu_mul=True)
+    rng = np.random.default_rng(21)
+    for m in (1, 3, 8, 12, 16, 37, 300):
+        x = rng.standard_normal((m, k)).astype(np.float16)
+        y = layer(gpu(x))
+        assert y.shape == (m, n // 2)
+        check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, m)
+    xu = torch.empty(3 * k + 1, device=DEV, dtype=torch.float16)[1:].view(3, k)
+    xn = rng.standard_normal((3, k)).astype(np.float16)
+    xu.copy_(gpu(xn))
+    check_close(layer(xu), o.swiglu_reference(xn, c.w_exact), 0.03, 0.02, "unaligned")
+
+
+def test_w4linear_gemm_switch_off(monkeypatch):
+    """TANDEM_W4_GEMM=0 sends M > 16 to dequantize + matmul (python/tandem/layers/awq.py:186)."""
+    layer, c = _layer(256, 128, seed=22)
+    monkeypatch.setattr(awq, "FUSED_GEMM", False)
+    x = np.random.default_rng(22).standard_normal((40, 256)).astype(np.float16)
+    check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, "switch off")

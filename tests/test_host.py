@@ -1,0 +1,208 @@
+"""Host-side logic that runs without a GPU: the C-ABI library and its exports, argument checks
+that return before any launch, the tile layout, the W4Linear contract and dispatch tables
+(python/tandem/layers/awq.py:136-286 and tests/test_awq.py of 12vivi/tandem are the models)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as o
+from tandem_amd.layers import awq, linear, w4_hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tandem_w4.h")
+
+
+def declared_symbols() -> list[str]:
+    text = open(HEADER, encoding="utf-8").read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tw4_\w+)\s*\(", text)))
+
+
+# ------------------------------------------------------------------------------------ C ABI
+def test_library_exports_every_declared_symbol():
+    syms = declared_symbols()
+    assert len(syms) >= 9
+    lib = w4_hip.library()
+    for name in syms:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", w4_hip.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (tw4_\w+)", out))
+    assert set(syms) == exported, (set(syms) ^ exported)
+
+
+def test_library_identity():
+    lib = w4_hip.library()
+    assert lib.tw4_arch() == b"gfx950"
+    assert lib.tw4_version().startswith(b"tandem_w4 ")
+
+
+def _fake(addr=4096):
+    return ctypes.c_void_p(addr)
+
+
+def test_argument_errors_return_before_launch():
+    """Each call fails a check that comes before any HIP call; the message names the problem
+    (the reference's TORCH_CHECK texts, python/tandem/csrc/w4_gemv.cu:568-579, 608, 624-625)."""
+    lib = w4_hip.library()
+    cases = [
+        (lambda: lib.tw4_dequant(_fake(), _fake(), _fake(), _fake(), 64, 100, 0, None), "K % 128"),
+        (lambda: lib.tw4_dequant(_fake(), _fake(), _fake(), _fake(), 60, 128, 0, None), "N % 8"),
+        (lambda: lib.tw4_dequant(_fake(), _fake(), _fake(), _fake(), 24, 128, 1, None), "deinterleave"),
+        (lambda: lib.tw4_dequant(None, _fake(), _fake(), _fake(), 64, 128, 0, None), "null"),
+        (lambda: lib.tw4_repack_awq(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 100, 64, 0, None), "K % 128"),
+        (lambda: lib.tw4_repack_awq(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 128, 24, 1, None), "interleave"),
+        (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 5, 64, 128, 4, 2, 1, None), "M <= 4"),
+        (lambda: lib.tw4_gemv(_fake(4100), _fake(), _fake(), _fake(), _fake(), 1, 64, 128, 4, 2, 1, None), "aligned"),
+        (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 17, 64, 128, 4, 2, 1, 0, None), "M <= 16"),
+        (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
+        (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
+                              32, 64, 128, 2, 1, 4, 1, 2, 17, 0, None), "splits"),
+        (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
+                              32, 64, 100, 2, 1, 4, 1, 2, 0, 0, None), "K % 128"),
+    ]
+    for call, needle in cases:
+        assert call() == w4_hip.TW4_EINVAL
+        assert needle in lib.tw4_last_error().decode(), (needle, lib.tw4_last_error())
+
+
+# ------------------------------------------------------------------------------ tile layout
+def decode_tile_layout(packed: np.ndarray, n: int, k: int) -> np.ndarray:
+    """Reads the tile layout back with the formula of include/tandem_w4.h: word (kb, r, s) of
+    block (T, g) holds k = 128 g + 32 kb + 8 s + 2 q + e of row 16 T + r in nibble q + 4 e."""
+    words = np.asarray(packed).view(np.uint32).reshape(-1)
+    g_count = k // 128
+    out = np.full((len(words) * 8 // k, k), -1, dtype=np.int64)
+    idx = np.arange(len(words))
+    blk, within = idx // 256, idx % 256
+    t, g = blk // g_count, blk % g_count
+    kb, r, s = within // 64, (within // 4) % 16, within % 4
+    for qq in range(4):
+        for e in range(2):
+            nib = (words >> (4 * (qq + 4 * e))) & 0xF
+            out[16 * t + r, 128 * g + 32 * kb + 8 * s + 2 * qq + e] = nib
+    assert (out >= 0).all()
+    return out
+
+
+@pytest.mark.parametrize("n,k", [(16, 128), (24, 256), (64, 384), (1000, 256)])
+def test_pack_rows_tile_layout(n, k):
+    q = torch.randint(0, 16, (n, k), dtype=torch.int32, generator=torch.Generator().manual_seed(n + k))
+    packed = awq.pack_rows(q)
+    assert packed.shape == (w4_hip.padded_rows(n), k // 8) and packed.dtype == torch.int32
+    got = decode_tile_layout(packed.numpy(), n, k)
+    assert (got[:n] == q.numpy()).all()
+    assert (got[n:] == 0).all()  # padding rows
+
+
+def test_pack_rows_known_positions():
+    """Spot checks in the style of tests/test_awq.py:58-65, on this build's layout."""
+    n, k = 32, 384
+    q = torch.randint(0, 16, (n, k), dtype=torch.int32)
+    packed = awq.pack_rows(q).view(n // 16, k // 128, 4, 16, 4)  # [T, g, kb, r, s]
+    for t, g, kb, r, s, qq, e in ((0, 0, 0, 0, 0, 0, 0), (1, 2, 3, 15, 3, 3, 1), (0, 1, 2, 7, 1, 2, 0)):
+        nib = (int(packed[t, g, kb, r, s]) >> (4 * (qq + 4 * e))) & 0xF
+        assert nib == int(q[16 * t + r, 128 * g + 32 * kb + 8 * s + 2 * qq + e])
+
+
+def test_unpack_awq_matches_oracle():
+    qw, _, _, q, _ = o.random_awq(256, 64, seed=11)
+    assert (awq.unpack_awq(torch.from_numpy(qw)).numpy() == q).all()
+
+
+def test_interleave_matches_oracle():
+    t = torch.arange(96 * 3).view(96, 3)
+    assert (awq.interleave_gate_up(t).numpy() == o.interleave_gate_up(t.numpy())).all()
+
+
+# ----------------------------------------------------------------------- W4Linear contract
+def test_w4linear_constructor_and_buffers():
+    layer = awq.W4Linear(512, 256, 128)
+    assert layer.awq_layout and not layer.silu_mul
+    assert layer.qweight.shape == (512, 32) and layer.qweight.dtype == torch.int32
+    assert layer.qzeros.shape == (4, 32) and layer.qzeros.dtype == torch.int32
+    assert layer.scales.shape == (4, 256) and layer.scales.dtype == torch.float16
+    for args in ((512, 256, 64), (500, 256, 128), (512, 252, 128)):
+        with pytest.raises(ValueError):
+            awq.W4Linear(*args)
+
+
+def test_enable_silu_mul_rules():
+    assert awq.W4Linear(512, 384, 128).enable_silu_mul()
+    assert not awq.W4Linear(512, 392, 128).enable_silu_mul()  # N % 16 != 0: not fusable
+
+
+def test_forward_needs_finalize_and_gpu():
+    layer = awq.W4Linear(256, 64, 128)
+    with pytest.raises(RuntimeError):
+        layer(torch.zeros(1, 256, dtype=torch.float16))
+    with pytest.raises(RuntimeError):  # finalize on CPU tensors: there is no CPU repack path
+        layer.finalize()
+
+
+def test_cpu_input_never_reaches_a_kernel():
+    ext = w4_hip.W4Extension()
+    x = torch.zeros(1, 128, dtype=torch.float16)
+    w = torch.zeros(16, 16, dtype=torch.int32)
+    s = torch.zeros(16, 1, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.w4_mma(x, w, s, s, 4, 2, 1, 0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        w4_hip.dequant(w, s, s)
+
+
+def test_pick_gemm_ladder():
+    table = ((17, "a"), (32, "b"), (1 << 30, None))
+    assert awq.pick_gemm(table, 17) == "a" and awq.pick_gemm(table, 18) == "b"
+    assert awq.pick_gemm(table, 4096) is None
+    assert awq.pick_gemm(((64, "x"),), 100) == "x"  # past the last m_max: the last entry
+
+
+def test_tables_are_well_formed():
+    kinds = {"gemv", "mma"}
+    assert awq.DEFAULT_KERNEL[0] in kinds and len(awq.DEFAULT_KERNEL) == 4
+    for table in awq.W4_KERNELS.values():
+        for key, cfg in table.items():
+            assert cfg[0] in kinds and len(cfg) == 4 and len(key) in (3, 4)
+    for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
+        m_maxes = [m for m, _ in ladder]
+        assert m_maxes == sorted(m_maxes)
+        for _, cfg in ladder:
+            assert cfg is None or len(cfg) == 6
+
+
+def test_make_linear_and_finalize_quantized():
+    class Q:
+        group_size = 128
+
+    assert isinstance(linear.make_linear(256, 64), torch.nn.Linear)
+    layer = linear.make_linear(256, 64, False, Q())
+    assert isinstance(layer, awq.W4Linear)
+    with pytest.raises(NotImplementedError):
+        linear.make_linear(256, 64, True, Q())
+    calls = []
+
+    class Fake(torch.nn.Module):
+        awq_layout = True
+
+        def finalize(self, name):
+            calls.append(name)
+            self.awq_layout = False
+
+    model = torch.nn.Sequential(Fake(), torch.nn.Linear(2, 2), Fake())
+    assert linear.finalize_quantized(model, "dev") == 2 and calls == ["dev", "dev"]
+    assert linear.finalize_quantized(model, "dev") == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                          text=True, timeout=300)
+    assert proc.returncode != 0 and "one GPU" in proc.stderr
