@@ -18,8 +18,9 @@
  *           weight o in nibble q + 4 e. One row tile x one group is 1 KB: one 16-byte load per
  *           lane of a 64-lane wavefront (lane 16 kb + r takes words s = 0..3). Rows n >= N
  *           are zero.
- *   scales  fp16 [N, K/128]    s[n, g]
- *   zeros   fp16 [N, K/128]    z[n, g], the integer zero point (exact)
+ *   scales  fp16 [N, K/128]    s[n, g], stored tile-major: at 16 T G + g rows_T + (n - 16 T),
+ *                              T = n / 16, rows_T = min(16, N - 16 T)
+ *   zeros   fp16 [N, K/128]    z[n, g], the integer zero point (exact), same order
  *   w[n, k] = fp16_rne((q[n, k] - z[n, k/128]) * s[n, k/128]).
  * N is the number of output features (the rows of scales); packed must hold Npad * K / 8 words.
  * The host view of `packed` is [Npad, K/8] int32: the same buffer size as the reference's
@@ -78,8 +79,9 @@ int tw4_dequant(const int32_t* packed, const uint16_t* scales, const uint16_t* z
                 uint16_t* out, int N, int K, int deinterleave, void* stream);
 
 /* Decode GEMV on the vector ALUs, 1 <= M <= 4: y fp16 [M, N]. x fp16 [M, K] contiguous and
- * 16-byte aligned. Config: warps_k wavefronts split K inside a workgroup, unroll quant groups
- * in flight per lane, ntile row tiles (16 rows) per wavefront.
+ * 16-byte aligned. Config: warps_k wavefronts split K into contiguous group ranges inside a
+ * workgroup, unroll quant groups per chunk (one chunk in flight ahead of the math), ntile row
+ * tiles (16 rows) per workgroup.
  * Replaces w4_gemv (python/tandem/csrc/w4_gemv.cu:96-153, 581-617). */
 int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              const uint16_t* zeros, uint16_t* y, int M, int N, int K,
@@ -113,6 +115,13 @@ int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              int64_t ws_floats, int64_t n_locks, int M, int N, int K,
              int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
              void* stream);
+
+/* Compiled configurations, for sweeps and tests (the reference lists them in its host code,
+ * python/tandem/csrc/w4_gemv.cu:596-597, 641-645, 676-679). Each writes up to max_configs
+ * tuples into out and returns how many exist: tw4_decode_configs (warps_k, unroll, ntile) for
+ * tw4_gemv and tw4_mma; tw4_gemm_configs (mt, nt, warps_n, warps_k, stages) for tw4_gemm. */
+int tw4_decode_configs(int* out, int max_configs);
+int tw4_gemm_configs(int* out, int max_configs);
 
 /* Grid the last tw4_gemm call on this thread launched: workgroups, data-parallel tiles and
  * split factor (for benchmarks and tests; the reference keeps these internal,

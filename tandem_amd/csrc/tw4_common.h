@@ -106,6 +106,17 @@ __device__ __forceinline__ f4 mfma16x16x32(const h8& a, const h8& b, const f4& c
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Scales and zeros are [N, K/128] fp16 buffers stored tile-major: the values of row tile T are
+// [group][row in tile], so the 16 rows of one group are 32 contiguous bytes (one load by a
+// wavefront touches one segment). Row tile T holds rows_t = min(16, N - 16 T) rows (only the last
+// tile of an N % 16 != 0 matrix has 8), and every earlier tile is full:
+//     offset(n, g) = 16 T G + g rows_t + (n - 16 T),   T = n / 16.
+__host__ __device__ __forceinline__ int tile_rows(int t, int n) { return min(16, n - 16 * t); }
+__host__ __device__ __forceinline__ int64_t param_offset(int row, int g, int n, int G) {
+    const int t = row >> 4;
+    return static_cast<int64_t>(16) * t * G + static_cast<int64_t>(g) * tile_rows(t, n) + (row & 15);
+}
+
 // Row of the interleave_gate_up order: destination row n' = 16 T + 8 h + i holds source row
 // h * N/2 + 8 T + i.
 __host__ __device__ __forceinline__ int interleaved_source_row(int nprime, int n) {

@@ -1,27 +1,34 @@
-// Decode kernels, M <= 16: y[M, N] = x[M, K] @ dequant(W)^T, bandwidth-bound on the int4 weights.
+// Decode kernels, M <= 16: y[M, N] = x[M, K] @ dequant(W)^T, bound by streaming the int4 weights.
 //
-// A workgroup owns NT row tiles (16 rows each) and its WK wavefronts split K by quant groups:
-// iteration i of wave w covers groups w + WK (u + UNROLL i), u = 0 .. UNROLL-1. Lane
-// l = 16 kb + r streams the 16 bytes (kb, r, s = 0..3) of each (row tile, group) block with one
-// non-temporal global_load_dwordx4: weights k = 128 g + 32 kb .. + 31 of row r. Weight blocks
-// and their scales / zeros are loaded one iteration ahead into a second register set (the loop
-// is unrolled by two so the sets swap roles without copies). Loads retire in issue order
-// (vmcnt), so each iteration first issues what it needs now (x), then the next iteration's
-// weights, then computes: waiting for x never waits for the prefetch. The partial sums of the
-// WK wavefronts are added in LDS at the end.
+// A workgroup owns NT row tiles (16 rows each); its WK wavefronts split K into WK contiguous ranges
+// of quant groups. Lane l = 16 kb + r streams the 16 bytes (kb, r, s = 0..3) of every (row tile,
+// group) block of its range with one non-temporal global_load_dwordx4 (weights k = 128 g + 32 kb
+// .. + 31 of row r), and the block's scale and zero with two 2-byte loads: scales and zeros are
+// stored tile-major, so the 16 rows of a group are one 32-byte segment. Ranges are walked in chunks
+// of UNROLL groups; the next chunk's weights, scales and zeros are in flight (a second register
+// set; the loop is unrolled by two so the sets swap roles without copies) while the current chunk is
+// computed. Loads retire in issue order, so a chunk issues what it needs now first, then the
+// prefetch, and no branch sits around a load: every wait is exact.
 //
-//   gemv: vector ALUs, M <= 4. x [M, K] is copied to LDS once per workgroup (all 16 lanes of a
-//         kb slice read the same 16 bytes: a broadcast). (q - z) is unpacked exactly to fp16
-//         pairs and multiplied with x pairs by v_dot2_f32_f16 (fp32 accumulation); the group's
-//         scale multiplies the lane's fp32 partial sum once per group. Row sums are finished
-//         with two cross-lane exchanges (lanes r, r + 16, r + 32, r + 48 hold the four 32-k
-//         slices of a group).
+// x is copied to LDS once per workgroup, while the first chunk is in flight, when it fits (row
+// stride K + 8 halves, so the 16 rows of a B-fragment read hit 16 different bank groups); the WK
+// partial sums are added in LDS at the end.
+//
+//   gemv: vector ALUs, M <= 4, x always in LDS, stored as x' (pairs 2, 3 and 6, 7 of every 8 k
+//         divided by 16) with per-slice sums of x' and x (fill_x_biased). A word becomes four
+//         fp16 pairs of "magic" values (1024 + q, or 1024 + 16 q for the high nibbles) with four
+//         v_and_or_b32 and one shift, and v_dot2_f32_f16 multiplies them with x' pairs (fp32
+//         accumulation); the 1024 bias and the zero point come off once per group and slice
+//         (dot - 1024 sum x' - z sum x), then the group's scale. Row sums are finished with two
+//         cross-lane exchanges (lanes r, r + 16, r + 32, r + 48 hold the four 32-k slices).
 //   mma:  matrix cores, M <= 16. v_mfma_f32_16x16x32_f16 with the dequantized weights
-//         fp16_rne((q - z) s) as A (16 rows x 32 k) and x as B (32 k x 16 batch columns, columns
-//         >= M are zero). Step s of a block uses word s of every lane: lane (kb, r) feeds A row r
-//         and B column r the weights / activations k = 128 g + 32 kb + 8 s .. + 7, the same k
-//         permutation for both operands, so each MFMA sums 32 distinct k of the group. D holds
-//         output rows 4 kb + i (i = 0..3) of batch column r in lane (kb, r).
+//         fp16_rne((q - z) s) as A (16 rows x 32 k) and x as B (32 k x 16 batch columns). Step s
+//         of a block uses word s of every lane: lane (kb, r) feeds A row r and B column r the
+//         weights / activations k = 128 g + 32 kb + 8 s .. + 7, the same k permutation for both
+//         operands, so each MFMA sums 32 distinct k of the group. B columns r >= M read row
+//         M - 1: they only feed D columns that are never stored. D holds output rows 4 kb + i
+//         (i = 0..3) of batch column r in lane (kb, r). x comes from LDS when M (K + 8) 2 bytes
+//         fit in 80 KB, else straight from global memory (issued before the prefetch).
 //   act = 1 (mma): rows are in interleave_gate_up order, so the gate rows 4 kb + i (kb = 0, 1)
 //         and up rows 8 + 4 kb + i of a feature sit in lanes l and l + 32; one cross-lane
 //         exchange pairs them and the lane writes silu(gate) * up.
@@ -30,78 +37,164 @@
 namespace tw4 {
 
 template <int U, int NT>
-struct WeightSet {  // one iteration's weight blocks and group parameters, per lane
+struct WeightSet {  // one chunk's weight blocks, scales and zeros, per lane
     u4 w[U][NT];
     uint32_t s[U][NT], z[U][NT];
 };
 
-template <int U, int NT>
-struct DecodeRows {
-    const u4* wb[NT];   // this lane's 16-byte vector of group 0 of each row tile
-    int64_t sb[NT];     // index of (row, group 0) in scales / zeros
+// The workgroup's row tiles. Everything but `lane` and `prow` is uniform across the wavefront (the
+// tile index comes from blockIdx), so tile and group offsets stay in scalar registers and each
+// load is one scalar base + the lane's fixed vector offset.
+template <int NT>
+struct TileStreams {
+    const u4* w[NT];     // group 0 block of the tile
+    int64_t p[NT];       // scale / zero offset of (tile, group 0) in the tile-major order
+    int rows[NT];        // rows of the tile: the scale / zero stride between groups
+    int prow[NT];        // this lane's row in the tile (clamped: padding rows have zero weights)
+    int lane;
 };
 
-template <int WK, int U, int NT>
-__device__ __forceinline__ void load_weights(WeightSet<U, NT>& ws, const DecodeRows<U, NT>& rows,
-                                             const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                             int wave, int iter, int G) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int g = min(wave + WK * (u + U * iter), G - 1);  // clamped: loaded, never used
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            ws.w[u][t] = load_stream(rows.wb[t] + static_cast<int64_t>(g) * kBlockU4);
-            ws.s[u][t] = load_u16(scales + rows.sb[t] + g);
-            ws.z[u][t] = load_u16(zeros + rows.sb[t] + g);
-        }
-    }
-}
-
-// Rows past N (the zero padding of the last row tile) read row N - 1's scale and zero: loaded
-// from a valid address, multiplied with zero weights, never stored.
-template <int U, int NT>
-__device__ __forceinline__ DecodeRows<U, NT> decode_rows(const u4* w, int tile0, int tiles, int N, int G, int lane) {
-    DecodeRows<U, NT> rows;
+template <int NT>
+__device__ __forceinline__ TileStreams<NT> tile_streams(const u4* w, int tile0, int tiles, int N, int G, int lane) {
+    TileStreams<NT> ts;
     const int r = lane & 15;
+    ts.lane = lane;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int tt = min(tile0 + t, tiles - 1);  // tiles past the end recompute the last one; not stored
-        rows.wb[t] = w + static_cast<int64_t>(tt) * G * kBlockU4 + lane;
-        rows.sb[t] = static_cast<int64_t>(min(16 * tt + r, N - 1)) * G;
+        ts.w[t] = w + static_cast<int64_t>(tt) * G * kBlockU4;
+        ts.rows[t] = tile_rows(tt, N);
+        ts.p[t] = static_cast<int64_t>(16) * tt * G;
+        ts.prow[t] = min(r, ts.rows[t] - 1);
     }
-    return rows;
+    return ts;
+}
+
+// LDS layout of a decode workgroup (offsets in 16-byte units): [x rows][corr][reduction].
+struct DecodeLds {
+    int xs;    // x row stride (u4): K / 8 + 1
+    int corr;  // gemv: per (m, group, slice) sums of x' and x (float2)
+    int red;   // cross-wavefront reduction
+    int total;
+};
+
+__host__ __device__ __forceinline__ DecodeLds decode_lds(bool xlds, int M, int K, int corr_u4, int red_u4) {
+    DecodeLds l;
+    l.xs = (K >> 3) + 1;
+    l.corr = xlds ? M * l.xs : 0;
+    l.red = l.corr + corr_u4;
+    l.total = l.red + red_u4;
+    return l;
+}
+
+__host__ __device__ __forceinline__ int gemv_corr_u4(int M, int K) { return M * (K >> 7) * 2; }  // float2 [M][G][4]
+__host__ __device__ __forceinline__ int gemv_red_u4(int M, int WK, int NT) { return (WK * NT * M * 16 + 3) / 4; }
+
+// One word -> its four magic halves, no zero applied: (1024 + q) for weights 0, 1 and 4, 5,
+// (1024 + 16 q) for weights 2, 3 and 6, 7 (see fill_x_biased).
+__device__ __forceinline__ void unpack_raw(uint32_t w, uint32_t magic, h2 (&d)[4]) {
+    const uint32_t w8 = w >> 8;
+    d[0] = bitcast<h2>((w & 0x000F000Fu) | magic);
+    d[1] = bitcast<h2>((w & 0x00F000F0u) | magic);
+    d[2] = bitcast<h2>((w8 & 0x000F000Fu) | magic);
+    d[3] = bitcast<h2>((w8 & 0x00F000F0u) | magic);
+}
+
+template <int U, int NT>
+__device__ __forceinline__ void load_chunk(WeightSet<U, NT>& ws, const TileStreams<NT>& ts, const uint16_t* s16,
+                                           const uint16_t* z16, int g0, int glast) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = min(g0 + u, glast);  // past the range: a valid block, given scale 0 below
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            ws.w[u][t] = load_stream(ts.w[t] + static_cast<int64_t>(g) * kBlockU4 + ts.lane);
+            const int64_t pg = ts.p[t] + static_cast<int64_t>(g) * ts.rows[t];
+            ws.s[u][t] = (s16 + pg)[ts.prow[t]];
+            ws.z[u][t] = (z16 + pg)[ts.prow[t]];
+        }
+    }
+}
+
+// x [M, K] -> LDS rows of K + 8 halves. Coalesced: consecutive threads read consecutive 16 bytes.
+__device__ __forceinline__ void fill_x(u4* smem, const DecodeLds& l, const h1* __restrict__ x, int M, int K,
+                                       int threads) {
+    const int kx = K >> 3;
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    for (int c = threadIdx.x; c < M * kx; c += threads) {
+        const int row = c / kx;
+        smem[row * l.xs + (c - row * kx)] = xg[c];
+    }
+}
+
+// x [M, K] -> LDS rows of K + 8 halves with every pair k = 8 j + 2, 3 and 8 j + 6, 7 divided by
+// 16 (x', exact: a power-of-two scale, rounded only where x / 16 is below fp16's normal range),
+// plus, per (m, group, 32-k slice kb), the float sums A = sum x' and B = sum x of the slice
+// (corr[(m G + g) 4 + kb], float2). A word's four magic halves (1024 + q for weights 8 j + 0, 1 and
+// 8 j + 4, 5; 1024 + 16 q for 8 j + 2, 3 and 8 j + 6, 7) dotted with x' give
+// sum q x + 1024 sum x', so sum (q - z) x = dot - 1024 A - z B.
+__device__ __forceinline__ void fill_x_biased(u4* smem, const DecodeLds& l, float2* corr, const h1* __restrict__ x,
+                                              int M, int K, int threads) {
+    const int kx = K >> 3;
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    const h2 lo = h2{static_cast<h1>(1.0f), static_cast<h1>(1.0f)};
+    const h2 hi = h2{static_cast<h1>(0.0625f), static_cast<h1>(0.0625f)};
+    for (int c = threadIdx.x; c < M * kx; c += threads) {  // M kx and threads are multiples of 4
+        const int row = c / kx, col = c - row * kx;
+        const u4 v = xg[c];
+        const h2 x0 = bitcast<h2>(v.x), x1 = bitcast<h2>(v.y), x2 = bitcast<h2>(v.z), x3 = bitcast<h2>(v.w);
+        const h2 y0 = x0 * lo, y1 = x1 * hi, y2 = x2 * lo, y3 = x3 * hi;
+        smem[row * l.xs + col] = u4{bitcast<uint32_t>(y0), bitcast<uint32_t>(y1), bitcast<uint32_t>(y2),
+                                    bitcast<uint32_t>(y3)};
+        float a = static_cast<float>(y0.x) + static_cast<float>(y0.y) + static_cast<float>(y1.x) +
+                  static_cast<float>(y1.y) + static_cast<float>(y2.x) + static_cast<float>(y2.y) +
+                  static_cast<float>(y3.x) + static_cast<float>(y3.y);
+        float b = static_cast<float>(x0.x) + static_cast<float>(x0.y) + static_cast<float>(x1.x) +
+                  static_cast<float>(x1.y) + static_cast<float>(x2.x) + static_cast<float>(x2.y) +
+                  static_cast<float>(x3.x) + static_cast<float>(x3.y);
+        // the four 16-byte chunks of a 32-k slice are lanes 4 i .. 4 i + 3 of this iteration
+        a += __shfl_xor(a, 1);
+        b += __shfl_xor(b, 1);
+        a += __shfl_xor(a, 2);
+        b += __shfl_xor(b, 2);
+        if ((col & 3) == 0) corr[row * (kx >> 2) + (col >> 2)] = float2{a, b};
+    }
+}
+
+__device__ __forceinline__ GroupQ group_q_raw(uint32_t s, uint32_t z, bool valid) {
+    return group_q(valid ? as_h1(s) : static_cast<h1>(0.0f), as_h1(z));
 }
 
 // ------------------------------------------------------------------------------------ gemv
-template <bool PF, int M, int WK, int U, int NT>
-__device__ __forceinline__ void gemv_step(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt,
-                                          const DecodeRows<U, NT>& rows, const u4* xs, const h1* scales,
-                                          const h1* zeros, float (&acc)[NT][M], int wave, int iter, int G,
-                                          int K, int kb, uint32_t magic) {
-    if constexpr (PF) load_weights<WK, U, NT>(nxt, rows, scales, zeros, wave, iter + 1, G);
+// The group's dot products run on the raw magic halves against x' (fill_x_biased): 4 v_and_or_b32,
+// one shift and 4 v_dot2 per word; the zero point and the 1024 bias come off once per group:
+// acc += s (dot - 1024 A - z B).
+template <bool PF, int M, int U, int NT>
+__device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
+                                           const uint16_t* s16, const uint16_t* z16, const u4* lx, const float2* corr,
+                                           const DecodeLds& l, float (&acc)[NT][M], int g0, int ge, int G, int kb,
+                                           uint32_t magic) {
+    if constexpr (PF) load_chunk<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math: the scheduler would sink it
 #pragma unroll
-    for (int u = 0; u < U; ++u) {  // no branch: a group past G (the wavefront's last iteration) gets scale 0
-        const int graw = wave + WK * (u + U * iter);
-        const bool valid = graw < G;
-        const int g = min(graw, G - 1);
-        GroupQ p[NT];
+    for (int u = 0; u < U; ++u) {
+        const int graw = g0 + u;
+        const bool valid = graw < ge;
+        const int g = min(graw, ge - 1);
         float part[NT][M];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            p[t] = group_q(as_h1(cur.s[u][t]), as_h1(cur.z[u][t]));
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int m = 0; m < M; ++m) part[t][m] = 0.0f;
-        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            u4 xq[M];  // x[m][128 g + 32 kb + 8 s .. + 7]
+            u4 xq[M];  // x'[m][128 g + 32 kb + 8 s .. + 7]
 #pragma unroll
-            for (int m = 0; m < M; ++m) xq[m] = xs[m * (K >> 3) + 16 * g + 4 * kb + s];
+            for (int m = 0; m < M; ++m) xq[m] = lx[m * l.xs + 16 * g + 4 * kb + s];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 h2 d[4];
-                unpack_qz(word_of(cur.w[u][t], s), p[t], magic, d);
+                unpack_raw(word_of(cur.w[u][t], s), magic, d);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     part[t][m] = __builtin_amdgcn_fdot2(d[0], bitcast<h2>(xq[m].x), part[t][m], false);
@@ -112,10 +205,15 @@ __device__ __forceinline__ void gemv_step(const WeightSet<U, NT>& cur, WeightSet
             }
         }
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float sc = valid ? static_cast<float>(as_h1(cur.s[u][t])) : 0.0f;
+        for (int m = 0; m < M; ++m) {
+            const float2 c = corr[(m * G + g) * 4 + kb];
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[t][m] = __builtin_fmaf(part[t][m], sc, acc[t][m]);
+            for (int t = 0; t < NT; ++t) {
+                const float sc = valid ? static_cast<float>(as_h1(cur.s[u][t])) : 0.0f;
+                const float zf = static_cast<float>(as_h1(cur.z[u][t]));
+                const float v = __builtin_fmaf(-zf, c.y, __builtin_fmaf(-1024.0f, c.x, part[t][m]));
+                acc[t][m] = __builtin_fmaf(v, sc, acc[t][m]);
+            }
         }
     }
 }
@@ -124,20 +222,23 @@ template <int M, int WK, int U, int NT>
 __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                       const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                       h1* __restrict__ y, int N, int K) {
-    extern __shared__ u4 xs[];  // x [M][K] as 16-byte chunks
-    __shared__ float red[WK][NT * M][16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    extern __shared__ u4 smem[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
     const int tile0 = blockIdx.x * NT;
+    const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, NT));
     const uint32_t magic = magic_reg();
-    const DecodeRows<U, NT> rows = decode_rows<U, NT>(w, tile0, tiles, N, G, lane);
-    const int iters = wave < G ? (G - wave + WK * U - 1) / (WK * U) : 0;
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
+    const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
+    const TileStreams<NT> ts = tile_streams<NT>(w, tile0, tiles, N, G, lane);
+    const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
+    const int nch = (ge - gb + U - 1) / U;
+    float2* corr = reinterpret_cast<float2*>(smem + l.corr);
 
     WeightSet<U, NT> a, b;
-    load_weights<WK, U, NT>(a, rows, scales, zeros, wave, 0, G);
-    const int chunks = M * (K >> 3);
-    for (int c = threadIdx.x; c < chunks; c += WK * 64) xs[c] = reinterpret_cast<const u4*>(x)[c];
+    if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+    fill_x_biased(smem, l, corr, x, M, K, WK * 64);
     __syncthreads();
 
     float acc[NT][M];
@@ -145,18 +246,17 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[t][m] = 0.0f;
-    // steady state: every step prefetches (no branch around the loads, so the waits stay exact);
-    // the last step of the wavefront prefetches nothing
+    // steady state: every chunk prefetches the next; the wavefront's last chunk prefetches nothing
     int i = 0;
-    for (; i + 2 < iters; i += 2) {
-        gemv_step<true, M, WK, U, NT>(a, b, rows, xs, scales, zeros, acc, wave, i, G, K, kb, magic);
-        gemv_step<true, M, WK, U, NT>(b, a, rows, xs, scales, zeros, acc, wave, i + 1, G, K, kb, magic);
+    for (; i + 2 < nch; i += 2) {
+        gemv_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, corr, l, acc, gb + U * i, ge, G, kb, magic);
+        gemv_chunk<true, M, U, NT>(b, a, ts, s16, z16, smem, corr, l, acc, gb + U * (i + 1), ge, G, kb, magic);
     }
-    if (i + 2 == iters) {
-        gemv_step<true, M, WK, U, NT>(a, b, rows, xs, scales, zeros, acc, wave, i, G, K, kb, magic);
-        gemv_step<false, M, WK, U, NT>(b, a, rows, xs, scales, zeros, acc, wave, i + 1, G, K, kb, magic);
-    } else if (i + 1 == iters) {
-        gemv_step<false, M, WK, U, NT>(a, b, rows, xs, scales, zeros, acc, wave, i, G, K, kb, magic);
+    if (i + 2 == nch) {
+        gemv_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, corr, l, acc, gb + U * i, ge, G, kb, magic);
+        gemv_chunk<false, M, U, NT>(b, a, ts, s16, z16, smem, corr, l, acc, gb + U * (i + 1), ge, G, kb, magic);
+    } else if (i + 1 == nch) {
+        gemv_chunk<false, M, U, NT>(a, b, ts, s16, z16, smem, corr, l, acc, gb + U * i, ge, G, kb, magic);
     }
     // lanes r, r + 16, r + 32, r + 48 hold the four k slices of row r
 #pragma unroll
@@ -169,11 +269,12 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
             acc[t][m] = v;
         }
     if (WK > 1) {
+        float* red = reinterpret_cast<float*>(smem + l.red);  // [WK][NT * M][16]
         if (kb == 0) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int m = 0; m < M; ++m) red[wave][t * M + m][r] = acc[t][m];
+                for (int m = 0; m < M; ++m) red[(wave * NT * M + t * M + m) * 16 + r] = acc[t][m];
         }
         __syncthreads();
         if (wave != 0) return;
@@ -182,7 +283,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int m = 0; m < M; ++m) acc[t][m] += red[v][t * M + m][r];
+                for (int m = 0; m < M; ++m) acc[t][m] += red[(v * NT * M + t * M + m) * 16 + r];
     }
     if (kb != 0) return;
 #pragma unroll
@@ -195,78 +296,95 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------- mma
-template <bool PF, int WK, int U, int NT>
-__device__ __forceinline__ void mma_step(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt,
-                                         const DecodeRows<U, NT>& rows, const h8* xl,
-                                         const h1* scales, const h1* zeros, f4 (&acc)[NT], int wave, int iter,
-                                         int G, uint32_t magic) {
-    h8 xb[U][4];  // issued first: waiting for it never waits for the prefetch below
+template <bool PF, bool XLDS, int U, int NT>
+__device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
+                                          const uint16_t* s16, const uint16_t* z16, const u4* smem, const DecodeLds& l,
+                                          const h8* xl, int xrow, f4 (&acc)[NT], int g0, int ge, int kb,
+                                          uint32_t magic) {
+    h8 xb[XLDS ? 1 : U][4];
+    if constexpr (!XLDS) {  // issued first: waiting for x never waits for the prefetch below
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        // k = 128 g + 32 kb + 8 s .. + 7. Lanes past M read row 0: B column r only feeds D column
-        // r, which is not stored for r >= M. A group past G (the wavefront's last iteration)
-        // reads group G - 1 and gets scale 0 below. No selects or branches around the loads, so
-        // the waits for x stay exact.
-        const int g = min(wave + WK * (u + U * iter), G - 1);
+        for (int u = 0; u < U; ++u) {
+            const int g = min(g0 + u, ge - 1);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) xb[u][s] = xl[16 * g + s];
+            for (int s = 0; s < 4; ++s) xb[u][s] = xl[16 * g + s];  // k = 128 g + 32 kb + 8 s .. + 7
+        }
     }
-    if constexpr (PF) load_weights<WK, U, NT>(nxt, rows, scales, zeros, wave, iter + 1, G);
+    if constexpr (PF) load_chunk<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads above the math: the scheduler would sink them
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const bool valid = wave + WK * (u + U * iter) < G;
+        const int graw = g0 + u;
+        const bool valid = graw < ge;
+        const int g = min(graw, ge - 1);
+        GroupQ p[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const GroupQ p = group_q(valid ? as_h1(cur.s[u][t]) : static_cast<h1>(0.0f), as_h1(cur.z[u][t]));
+        for (int t = 0; t < NT; ++t) p[t] = group_q_raw(cur.s[u][t], cur.z[u][t], valid);
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                acc[t] = mfma16x16x32(dequant_word(word_of(cur.w[u][t], s), p, magic), xb[u][s], acc[t]);
+        for (int s = 0; s < 4; ++s) {
+            h8 xv;
+            if constexpr (XLDS)
+                xv = bitcast<h8>(smem[xrow * l.xs + 16 * g + 4 * kb + s]);
+            else
+                xv = xb[u][s];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(dequant_word(word_of(cur.w[u][t], s), p[t], magic), xv, acc[t]);
         }
     }
 }
 
-template <int WK, int U, int NT>
+template <int WK, int U, int NT, bool XLDS>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                      h1* __restrict__ y, int M, int N, int K, int act) {
-    __shared__ f4 red[WK > 1 ? WK - 1 : 1][NT][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    extern __shared__ u4 smem[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
     const int tile0 = blockIdx.x * NT;
+    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * 64);
     const uint32_t magic = magic_reg();
-    const DecodeRows<U, NT> rows = decode_rows<U, NT>(w, tile0, tiles, N, G, lane);
-    const int iters = wave < G ? (G - wave + WK * U - 1) / (WK * U) : 0;
-    const h8* xl = reinterpret_cast<const h8*>(x + static_cast<int64_t>(r < M ? r : 0) * K + 32 * kb);
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
+    const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
+    const TileStreams<NT> ts = tile_streams<NT>(w, tile0, tiles, N, G, lane);
+    const int xrow = min(r, M - 1);  // B columns r >= M: any valid row, their D columns are not stored
+    const h8* xl = reinterpret_cast<const h8*>(x + static_cast<int64_t>(xrow) * K + 32 * kb);
+    const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
+    const int nch = (ge - gb + U - 1) / U;
 
     WeightSet<U, NT> a, b;
-    load_weights<WK, U, NT>(a, rows, scales, zeros, wave, 0, G);
+    if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+    if constexpr (XLDS) {
+        fill_x(smem, l, x, M, K, WK * 64);
+        __syncthreads();
+    }
+
     f4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
-    for (; i + 2 < iters; i += 2) {
-        mma_step<true, WK, U, NT>(a, b, rows, xl, scales, zeros, acc, wave, i, G, magic);
-        mma_step<true, WK, U, NT>(b, a, rows, xl, scales, zeros, acc, wave, i + 1, G, magic);
+    for (; i + 2 < nch; i += 2) {
+        mma_chunk<true, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<true, XLDS, U, NT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
     }
-    if (i + 2 == iters) {
-        mma_step<true, WK, U, NT>(a, b, rows, xl, scales, zeros, acc, wave, i, G, magic);
-        mma_step<false, WK, U, NT>(b, a, rows, xl, scales, zeros, acc, wave, i + 1, G, magic);
-    } else if (i + 1 == iters) {
-        mma_step<false, WK, U, NT>(a, b, rows, xl, scales, zeros, acc, wave, i, G, magic);
+    if (i + 2 == nch) {
+        mma_chunk<true, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XLDS, U, NT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+    } else if (i + 1 == nch) {
+        mma_chunk<false, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
     }
     if (WK > 1) {
+        f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][64]
         if (wave > 0) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
+            for (int t = 0; t < NT; ++t) red[((wave - 1) * NT + t) * 64 + lane] = acc[t];
         }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int v = 0; v < WK - 1; ++v)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] += red[v][t][lane];
+            for (int t = 0; t < NT; ++t) acc[t] += red[(v * NT + t) * 64 + lane];
     }
     const int m = r;
     if (act) {  // N % 16 == 0 (checked on the host)
@@ -299,26 +417,20 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
 }
 
 // Compiled decode configurations (warps_k, unroll, ntile).
-#define TW4_DECODE_CONFIGS(X) \
-    X(1, 2, 1) X(1, 4, 1) X(2, 2, 1) X(2, 4, 1) X(4, 1, 1) X(4, 2, 1) X(4, 4, 1) X(8, 1, 1) X(8, 2, 1) \
-    X(2, 2, 2) X(4, 1, 2) X(4, 2, 2) X(8, 1, 2) X(8, 2, 2) X(4, 4, 2) X(2, 4, 2) X(16, 1, 1) X(16, 2, 1)
+#define TW4_DECODE_CONFIGS(X)                                                                            \
+    X(1, 4, 1) X(1, 8, 1) X(2, 4, 1) X(2, 8, 1) X(4, 1, 1) X(4, 2, 1) X(4, 4, 1) X(4, 8, 1) X(8, 1, 1) \
+    X(8, 2, 1) X(8, 4, 1) X(16, 1, 1) X(16, 2, 1) X(2, 4, 2) X(4, 2, 2) X(4, 4, 2) X(8, 1, 2) X(8, 2, 2)
 
 constexpr int kMaxDevices = 64;
-constexpr int kGemvMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
+constexpr int kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
+constexpr int kXLdsLimit = 80 * 1024;    // mma keeps x in LDS up to this size (M = 8 at K = 4096)
 static int g_decode_ready[kMaxDevices];
 
-template <int M>
-int gemv_prepare() {
-#define TW4_GEMV_ATTR(WK, U, T)                                                                          \
-    {                                                                                                    \
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_kernel<M, WK, U, T>),      \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,                   \
-                                           kGemvMaxLds - static_cast<int>(sizeof(float)) * WK * T * M * 16); \
-        if (e != hipSuccess) return tw4host::hip_fail(e, "init: gemv hipFuncSetAttribute");             \
-    }
-    TW4_DECODE_CONFIGS(TW4_GEMV_ATTR)
-#undef TW4_GEMV_ATTR
-    return TW4_OK;
+template <typename Kern>
+int allow_lds(Kern kern) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       kMaxLds);
+    return e == hipSuccess ? TW4_OK : tw4host::hip_fail(e, "init: decode hipFuncSetAttribute");
 }
 
 int decode_prepare(int dev) {
@@ -327,26 +439,40 @@ int decode_prepare(int dev) {
         return TW4_EINVAL;
     }
     if (g_decode_ready[dev]) return TW4_OK;
-    int rc = gemv_prepare<1>();
-    if (rc == TW4_OK) rc = gemv_prepare<2>();
-    if (rc == TW4_OK) rc = gemv_prepare<3>();
-    if (rc == TW4_OK) rc = gemv_prepare<4>();
+    int rc = TW4_OK;
+#define TW4_ATTR(WK, U, T)                                                   \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<1, WK, U, T>);              \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<2, WK, U, T>);              \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<3, WK, U, T>);              \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<4, WK, U, T>);              \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, true>);            \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, false>);
+    TW4_DECODE_CONFIGS(TW4_ATTR)
+#undef TW4_ATTR
     if (rc == TW4_OK) g_decode_ready[dev] = 1;
     return rc;
+}
+
+int ensure_prepared() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "decode: hipGetDevice");
+    if (dev >= 0 && dev < kMaxDevices && g_decode_ready[dev]) return TW4_OK;
+    return decode_prepare(dev);
 }
 
 template <int M>
 int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
                   hipStream_t st) {
     const int tiles = (N + 15) >> 4;
-    const size_t lds = static_cast<size_t>(M) * K * 2;
-#define TW4_GEMV_CASE(WK, U, T)                                                                     \
-    if (wk == WK && un == U && nt == T) {                                                           \
-        TW4_REQUIRE(lds + sizeof(float) * WK * T * M * 16 <= static_cast<size_t>(kGemvMaxLds), TW4_EINVAL, \
-                    "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);                        \
-        gemv_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K);   \
-        TW4_LAUNCH_CHECK("gemv: launch");                                                           \
-        return TW4_OK;                                                                              \
+#define TW4_GEMV_CASE(WK, U, T)                                                                              \
+    if (wk == WK && un == U && nt == T) {                                                                    \
+        const size_t lds = 16 * static_cast<size_t>(decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, T)).total); \
+        TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
+                    "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);          \
+        gemv_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K);            \
+        TW4_LAUNCH_CHECK("gemv: launch");                                                                    \
+        return TW4_OK;                                                                                       \
     }
     TW4_DECODE_CONFIGS(TW4_GEMV_CASE)
 #undef TW4_GEMV_CASE
@@ -376,13 +502,8 @@ extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t
     int rc = check_operands("gemv", x, packed, scales, zeros, y, M, N, K);
     if (rc) return rc;
     TW4_REQUIRE(M >= 1 && M <= 4, TW4_EINVAL, "gemv: 1 <= M <= 4 (M = %d; larger M: mma)", M);
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return tw4host::hip_fail(e, "gemv: hipGetDevice");
-    if (dev < 0 || dev >= kMaxDevices || !g_decode_ready[dev]) {
-        rc = decode_prepare(dev);
-        if (rc) return rc;
-    }
+    rc = ensure_prepared();
+    if (rc) return rc;
     auto xp = reinterpret_cast<const h1*>(x);
     auto wp = reinterpret_cast<const u4*>(packed);
     auto sp = reinterpret_cast<const h1*>(scales);
@@ -404,6 +525,8 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
     TW4_REQUIRE(M >= 1 && M <= 16, TW4_EINVAL, "mma: 1 <= M <= 16 (M = %d)", M);
     TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
                 "mma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    rc = ensure_prepared();
+    if (rc) return rc;
     auto xp = reinterpret_cast<const h1*>(x);
     auto wp = reinterpret_cast<const u4*>(packed);
     auto sp = reinterpret_cast<const h1*>(scales);
@@ -411,14 +534,33 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
     const int tiles = (N + 15) >> 4;
-#define TW4_MMA_CASE(WK, U, T)                                                                               \
-    if (warps_k == WK && unroll == U && ntile == T) {                                                        \
-        mma_kernel<WK, U, T><<<(tiles + T - 1) / T, WK * 64, 0, st>>>(xp, wp, sp, zp, yp, M, N, K, act);     \
-        TW4_LAUNCH_CHECK("mma: launch");                                                                     \
-        return TW4_OK;                                                                                       \
+    const bool xlds = static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+#define TW4_MMA_CASE(WK, U, T)                                                                                \
+    if (warps_k == WK && unroll == U && ntile == T) {                                                         \
+        const size_t lds = 16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * 64).total);     \
+        if (xlds)                                                                                             \
+            mma_kernel<WK, U, T, true><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act); \
+        else                                                                                                  \
+            mma_kernel<WK, U, T, false><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act); \
+        TW4_LAUNCH_CHECK("mma: launch");                                                                      \
+        return TW4_OK;                                                                                        \
     }
     TW4_DECODE_CONFIGS(TW4_MMA_CASE)
 #undef TW4_MMA_CASE
     tw4host::set_error("mma: unsupported warps_k / unroll / ntile %d / %d / %d", warps_k, unroll, ntile);
     return TW4_ECONFIG;
+}
+
+extern "C" int tw4_decode_configs(int* out, int max_configs) {
+    int n = 0;
+#define TW4_LIST(WK, U, T)                  \
+    if (out && n < max_configs) {           \
+        out[3 * n] = WK;                    \
+        out[3 * n + 1] = U;                 \
+        out[3 * n + 2] = T;                 \
+    }                                       \
+    ++n;
+    TW4_DECODE_CONFIGS(TW4_LIST)
+#undef TW4_LIST
+    return n;
 }

@@ -92,12 +92,14 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
     }
     // weight blocks and group parameters of this wavefront's row tiles
     const u4* wb[NT];
-    int64_t sb[NT];
+    int64_t sb[NT];  // tile-major scale / zero offset of group 0 (row r clamped to the tile: padding rows
+    int srows[NT];   // have zero weights and are never stored), and the stride between groups
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int tt = min(wt0 + t, tiles_n - 1);
         wb[t] = w + static_cast<int64_t>(tt) * G * kBlockU4 + lane;
-        sb[t] = static_cast<int64_t>(min(16 * tt + r, N - 1)) * G;  // padding rows: row N - 1's, never stored
+        srows[t] = tile_rows(tt, N);
+        sb[t] = static_cast<int64_t>(16) * tt * G + min(r, srows[t] - 1);
     }
     const uint32_t magic = magic_reg();
 
@@ -124,8 +126,8 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             ws.w[t] = load_stream(wb[t] + static_cast<int64_t>(g) * kBlockU4);
-            ws.s[t] = load_u16(scales + sb[t] + g);
-            ws.z[t] = load_u16(zeros + sb[t] + g);
+            ws.s[t] = load_u16(scales + sb[t] + static_cast<int64_t>(g) * srows[t]);
+            ws.z[t] = load_u16(zeros + sb[t] + static_cast<int64_t>(g) * srows[t]);
         }
     };
 
@@ -432,4 +434,20 @@ extern "C" int tw4_gemm_last_grid(int* blocks, int* dp_tiles, int* splits) {
     if (dp_tiles) *dp_tiles = g_last_dp;
     if (splits) *splits = g_last_splits;
     return TW4_OK;
+}
+
+extern "C" int tw4_gemm_configs(int* out, int max_configs) {
+    int n = 0;
+#define TW4_LIST(MT, NT, WN, WK, ST)      \
+    if (out && n < max_configs) {         \
+        out[5 * n] = MT;                  \
+        out[5 * n + 1] = NT;              \
+        out[5 * n + 2] = WN;              \
+        out[5 * n + 3] = WK;              \
+        out[5 * n + 4] = ST;              \
+    }                                     \
+    ++n;
+    TW4_GEMM_CONFIGS(TW4_LIST)
+#undef TW4_LIST
+    return n;
 }

@@ -38,7 +38,8 @@ __global__ void repack_weights_kernel(const int32_t* __restrict__ qweight, uint3
     }
 }
 
-// One thread per (group, column): scales [G, N] -> [N, G]; qzeros nibble -> exact fp16 zero.
+// One thread per (group, column): scales [G, N] -> tile-major [N, G] (param_offset); qzeros nibble ->
+// exact fp16 zero.
 __global__ void repack_group_params_kernel(const int32_t* __restrict__ qzeros, const h1* __restrict__ scales,
                                           h1* __restrict__ s_out, h1* __restrict__ z_out, int K, int N,
                                           int interleave) {
@@ -49,8 +50,9 @@ __global__ void repack_group_params_kernel(const int32_t* __restrict__ qzeros, c
     const uint32_t zw = static_cast<uint32_t>(qzeros[static_cast<int64_t>(g) * (N >> 3) + (n >> 3)]);
     const int z = static_cast<int>((zw >> (4 * kAwqReverse[n & 7])) & 0xFu);
     const int dst = interleave ? interleaved_dest_row(n, N) : n;
-    s_out[static_cast<int64_t>(dst) * G + g] = scales[idx];
-    z_out[static_cast<int64_t>(dst) * G + g] = static_cast<h1>(static_cast<float>(z));
+    const int64_t o = param_offset(dst, g, N, G);
+    s_out[o] = scales[idx];
+    z_out[o] = static_cast<h1>(static_cast<float>(z));
 }
 
 // One thread per 16-byte vector of the tile layout (lane l = 16 kb + r of its block): writes the
@@ -69,7 +71,7 @@ __global__ void dequant_kernel(const u4* __restrict__ packed, const h1* __restri
     if (row >= N) return;
     const uint32_t magic = magic_reg();
     const u4 v = packed[idx];
-    const int64_t sidx = static_cast<int64_t>(row) * G + g;
+    const int64_t sidx = param_offset(row, g, N, G);
     const GroupQ p = group_q(scales[sidx], zeros[sidx]);
     const int dst = deinterleave ? interleaved_source_row(row, N) : row;
     h8* o = reinterpret_cast<h8*>(out + static_cast<int64_t>(dst) * K + 128 * g + 32 * kb);

@@ -17,7 +17,9 @@ and w[k, n] = (q[k, n] - z[k // G, n]) * s[k // G, n].
            k = 128 g + 32 kb + 8 s + 2 q + e (q = 0..3, e = 0..1) of row 16 T + r in nibble q + 4 e;
            one (row tile, group) block is 1 KB, read by one 64-lane wavefront with one 16-byte
            load per lane (lane 16 kb + r). Rows >= N are zero.
-    scales [N, K/G] float16, zeros [N, K/G] float16 (the integer zero point, exact)
+    scales [N, K/G] float16, zeros [N, K/G] float16 (the integer zero point, exact), both stored
+           tile-major (tile_major_params): a row tile's values as [group][row], so a wavefront's
+           per-group load of 16 rows' scales is one 32-byte segment
 The nibble order inside a word is the reference's (python/tandem/layers/awq.py:12-20); the word
 order is this build's (the reference keeps each row contiguous: [N][K/G][4 j][4 cc]).
 
@@ -65,11 +67,35 @@ def pack_rows(q: torch.Tensor) -> torch.Tensor:
     return words.reshape(npad, k // 8).to(torch.int32)
 
 
+def tile_major_params(t: torch.Tensor) -> torch.Tensor:
+    """Row-major [N, K/G] scales / zeros -> the kernels' tile-major order, same shape: row tile T
+    (16 rows, or the N - 16 T left over) stored as [group][row], so one group's rows are
+    contiguous (offset 16 T G + g rows_T + r). A layout utility on any device."""
+    n, g = t.shape
+    full = n // 16 * 16
+    parts = [t[:full].reshape(n // 16, 16, g).transpose(1, 2).reshape(-1)]
+    if full < n:
+        parts.append(t[full:].t().reshape(-1))
+    return torch.cat(parts).reshape(n, g)
+
+
+def row_major_params(t: torch.Tensor) -> torch.Tensor:
+    """Inverse of tile_major_params."""
+    n, g = t.shape
+    full = n // 16 * 16
+    flat = t.reshape(-1)
+    parts = [flat[:full * g].reshape(n // 16, g, 16).transpose(1, 2).reshape(full, g)]
+    if full < n:
+        parts.append(flat[full * g:].reshape(g, n - full).t())
+    return torch.cat(parts)
+
+
 def repack_awq(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group: int,
                dtype: torch.dtype = torch.float16, interleave: bool = False
                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """AWQ (qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N]) -> tile layout (packed [Npad, K/8]
-    int32, scales [N, K/G], zeros [N, K/G]) on the GPU (python/tandem/layers/awq.py:60-68).
+    int32, scales [N, K/G] and zeros [N, K/G] in tile-major order) on the GPU
+    (python/tandem/layers/awq.py:60-68).
     ``interleave``: rows in interleave_gate_up order (the reference applies interleave_gate_up to
     the repacked rows, awq.py:237-238; the tile layout takes it inside the repack kernel)."""
     if group != 128 or qweight.shape[0] % 128 or scales.shape != (qweight.shape[0] // group, 8 * qweight.shape[1]):
@@ -83,7 +109,8 @@ def interleave_gate_up(t: torch.Tensor) -> torch.Tensor:
     """Rows [gate (I); up (I)] -> tiles of 16 rows [gate 8i .. 8i+7, up 8i .. 8i+7], the order in
     which the matrix-core kernels' SwiGLU epilogue finds gate and up of a feature in lanes l and
     l + 32 (python/tandem/layers/awq.py:71-75). For row-major tensors (scales, zeros, dense
-    weights); the tile-layout `packed` is interleaved by repack_awq(..., interleave=True)."""
+    weights, before tile_major_params); the tile-layout `packed` is interleaved by
+    repack_awq(..., interleave=True)."""
     n = t.shape[0]
     return t.view(2, n // 16, 8, *t.shape[1:]).transpose(0, 1).reshape(t.shape)
 

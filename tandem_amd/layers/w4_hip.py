@@ -46,6 +46,8 @@ _SIGNATURES = {
     "tw4_mma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
+    "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
+    "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
 }
 
 
@@ -60,6 +62,24 @@ def library() -> ctypes.CDLL:
         fn.argtypes = args
         fn.restype = res
     return lib
+
+
+def _configs(name: str, width: int) -> tuple[tuple[int, ...], ...]:
+    fn = getattr(library(), name)
+    n = fn(None, 0)
+    buf = (_I * (width * n))()
+    fn(buf, n)
+    return tuple(tuple(buf[width * i + j] for j in range(width)) for i in range(n))
+
+
+def decode_configs() -> tuple[tuple[int, int, int], ...]:
+    """The compiled (warps_k, unroll, ntile) configurations of w4_gemv / w4_mma."""
+    return _configs("tw4_decode_configs", 3)
+
+
+def gemm_configs() -> tuple[tuple[int, int, int, int, int], ...]:
+    """The compiled (mt, nt, warps_n, warps_k, stages) configurations of w4_gemm."""
+    return _configs("tw4_gemm_configs", 5)
 
 
 def check(status: int) -> None:

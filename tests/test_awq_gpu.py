@@ -23,12 +23,8 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 SHAPES = ((128, 24), (256, 520), (1024, 64), (4096, 1000))  # (K, N); N % 16 != 0 exercises the padded tile
-DECODE_CONFIGS = ((1, 2, 1), (1, 4, 1), (2, 2, 1), (2, 4, 1), (4, 1, 1), (4, 2, 1), (4, 4, 1), (8, 1, 1), (8, 2, 1),
-                  (2, 2, 2), (4, 1, 2), (4, 2, 2), (8, 1, 2), (8, 2, 2), (4, 4, 2), (2, 4, 2), (16, 1, 1),
-                  (16, 2, 1))  # (warps_k, unroll, ntile)
-GEMM_CONFIGS = ((1, 1, 4, 1, 2), (1, 2, 4, 1, 2), (2, 1, 4, 1, 2), (2, 2, 4, 1, 2), (2, 1, 4, 2, 2), (2, 2, 4, 2, 2),
-                (4, 1, 4, 1, 2), (4, 2, 4, 1, 2), (4, 2, 4, 2, 2), (4, 4, 4, 1, 2), (8, 1, 4, 1, 2), (8, 2, 4, 1, 2),
-                (8, 4, 4, 1, 2), (8, 2, 2, 1, 2), (4, 4, 2, 1, 2))  # (MT, NT, WARPS_N, WARPS_K, STAGES)
+DECODE_CONFIGS = w4_hip.decode_configs()  # every compiled (warps_k, unroll, ntile)
+GEMM_CONFIGS = w4_hip.gemm_configs()      # every compiled (MT, NT, WARPS_N, WARPS_K, STAGES)
 
 
 @pytest.fixture(scope="module")
@@ -77,8 +73,8 @@ def test_repack_and_dequant_bit_exact(k, n):
     checks atol 1e-3; here the bar is equality)."""
     c = Case(k, n, seed=k + n)
     assert c.packed.shape == (w4_hip.padded_rows(n), k // 8) and c.s.shape == (n, k // 128)
-    assert torch.equal(c.s.cpu(), torch.from_numpy(c.scales.T.copy()))
-    assert torch.equal(c.zz.cpu(), torch.from_numpy(c.z.T.astype(np.float16).copy()))
+    assert torch.equal(c.s.cpu(), awq.tile_major_params(torch.from_numpy(c.scales.T.copy())))
+    assert torch.equal(c.zz.cpu(), awq.tile_major_params(torch.from_numpy(c.z.T.astype(np.float16).copy())))
     assert torch.equal(c.packed.cpu(), awq.pack_rows(torch.from_numpy(c.q.T.copy())))
     w = awq.w4_dequant(c.packed, c.s, c.zz)
     assert w.shape == (n, k)
@@ -98,7 +94,7 @@ def test_dequant_deinterleave():
     c = Case(256, 96, seed=7)
     pi, si, zi = w4_hip.repack(gpu(c.qweight), gpu(c.qzeros), gpu(c.scales), interleave=True)
     assert torch.equal(awq.w4_dequant(pi, si, zi, deinterleave=True), awq.w4_dequant(c.packed, c.s, c.zz))
-    assert torch.equal(si, awq.interleave_gate_up(c.s))
+    assert torch.equal(si, awq.tile_major_params(awq.interleave_gate_up(awq.row_major_params(c.s))))
     q_rows = torch.from_numpy(o.interleave_gate_up(c.q.T.copy()))
     assert torch.equal(pi.cpu(), awq.pack_rows(q_rows))
 

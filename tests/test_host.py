@@ -39,6 +39,14 @@ def test_library_exports_every_declared_symbol():
     assert set(syms) == exported, (set(syms) ^ exported)
 
 
+def test_config_queries():
+    dec, gemm = w4_hip.decode_configs(), w4_hip.gemm_configs()
+    assert len(dec) >= 8 and all(len(c) == 3 and c[0] >= 1 and c[1] >= 1 for c in dec)
+    assert len(gemm) >= 8 and all(len(c) == 5 and c[3] in (1, 2) for c in gemm)
+    assert awq.DEFAULT_KERNEL[1:] in dec
+    assert all(cfg[:5] in gemm for _, cfg in awq.DEFAULT_GEMM if cfg is not None)
+
+
 def test_library_identity():
     lib = w4_hip.library()
     assert lib.tw4_arch() == b"gfx950"
@@ -111,6 +119,22 @@ def test_pack_rows_known_positions():
     for t, g, kb, r, s, qq, e in ((0, 0, 0, 0, 0, 0, 0), (1, 2, 3, 15, 3, 3, 1), (0, 1, 2, 7, 1, 2, 0)):
         nib = (int(packed[t, g, kb, r, s]) >> (4 * (qq + 4 * e))) & 0xF
         assert nib == int(q[16 * t + r, 128 * g + 32 * kb + 8 * s + 2 * qq + e])
+
+
+@pytest.mark.parametrize("n,g", [(16, 1), (48, 32), (24, 8), (1000, 3)])
+def test_tile_major_params(n, g):
+    """Scales / zeros order of include/tandem_w4.h: value (row, group) at
+    16 T G + g rows_T + (row - 16 T), T = row / 16, rows_T = min(16, N - 16 T)."""
+    t = torch.arange(n * g, dtype=torch.int64).view(n, g)
+    tm = awq.tile_major_params(t)
+    assert tm.shape == (n, g)
+    flat = tm.reshape(-1)
+    for row in range(n):
+        tt = row // 16
+        rows = min(16, n - 16 * tt)
+        for gg in range(g):
+            assert int(flat[16 * tt * g + gg * rows + row - 16 * tt]) == int(t[row, gg])
+    assert torch.equal(awq.row_major_params(tm), t)
 
 
 def test_unpack_awq_matches_oracle():
