@@ -1,4 +1,4 @@
-// Decode kernels, M <= 16: y[M, N] = x[M, K] @ dequant(W)^T, bound by streaming the int4 weights.
+// Decode kernels, M <= 64: y[M, N] = x[M, K] @ dequant(W)^T, bound by streaming the int4 weights.
 //
 // A workgroup owns NT row tiles (16 rows each); its WK wavefronts split K into WK contiguous ranges
 // of quant groups. Lane l = 16 kb + r streams the 16 bytes (kb, r, s = 0..3) of every (row tile,
@@ -21,7 +21,7 @@
 //         accumulation); the 1024 bias and the zero point come off once per group and slice
 //         (dot - 1024 sum x' - z sum x), then the group's scale. Row sums are finished with two
 //         cross-lane exchanges (lanes r, r + 16, r + 32, r + 48 hold the four 32-k slices).
-//   mma:  matrix cores, M <= 16. v_mfma_f32_16x16x32_f16 with the dequantized weights
+//   mma:  matrix cores, M <= 64 (MT = ceil(M / 16) batch tiles of 16 columns). v_mfma_f32_16x16x32_f16 with the dequantized weights
 //         fp16_rne((q - z) s) as A (16 rows x 32 k) and x as B (32 k x 16 batch columns). Step s
 //         of a block uses word s of every lane: lane (kb, r) feeds A row r and B column r the
 //         weights / activations k = 128 g + 32 kb + 8 s .. + 7, the same k permutation for both
@@ -296,18 +296,23 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------- mma
-template <bool PF, bool XLDS, int U, int NT>
+// MT batch tiles of 16 columns (M <= 16 MT): lane (kb, r) feeds B column r of tile b = token
+// 16 b + r, and D tile (t, b) holds rows 4 kb + i of that token. Each dequantized A fragment feeds
+// MT MFMAs.
+template <bool PF, bool XLDS, int U, int NT, int MT>
 __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
                                           const uint16_t* s16, const uint16_t* z16, const u4* smem, const DecodeLds& l,
-                                          const h8* xl, int xrow, f4 (&acc)[NT], int g0, int ge, int kb,
-                                          uint32_t magic) {
-    h8 xb[XLDS ? 1 : U][4];
+                                          const h8* const (&xl)[MT], int xrow, f4 (&acc)[NT][MT], int g0, int ge,
+                                          int kb, uint32_t magic) {
+    h8 xb[XLDS ? 1 : U][4][MT];
     if constexpr (!XLDS) {  // issued first: waiting for x never waits for the prefetch below
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int g = min(g0 + u, ge - 1);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) xb[u][s] = xl[16 * g + s];  // k = 128 g + 32 kb + 8 s .. + 7
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) xb[u][s][b] = xl[b][16 * g + s];  // k = 128 g + 32 kb + 8 s .. + 7
         }
     }
     if constexpr (PF) load_chunk<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1);
@@ -322,33 +327,47 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
         for (int t = 0; t < NT; ++t) p[t] = group_q_raw(cur.s[u][t], cur.z[u][t], valid);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            h8 xv;
-            if constexpr (XLDS)
-                xv = bitcast<h8>(smem[xrow * l.xs + 16 * g + 4 * kb + s]);
-            else
-                xv = xb[u][s];
+            h8 xv[MT];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(dequant_word(word_of(cur.w[u][t], s), p[t], magic), xv, acc[t]);
+            for (int b = 0; b < MT; ++b) {
+                if constexpr (XLDS)
+                    xv[b] = bitcast<h8>(smem[xrow * l.xs + 16 * g + 4 * kb + s]);
+                else
+                    xv[b] = xb[u][s][b];
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const h8 wa = dequant_word(word_of(cur.w[u][t], s), p[t], magic);
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = mfma16x16x32(wa, xv[b], acc[t][b]);
+            }
         }
     }
 }
 
-template <int WK, int U, int NT, bool XLDS>
+template <int WK, int U, int NT, int MT, bool XLDS>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                      h1* __restrict__ y, int M, int N, int K, int act) {
+    static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
+    if constexpr (U * MT > 4 && MT > 1) {
+        return;  // register budget: never launched (tw4_mma rejects U * MT > 4 for M > 16)
+    } else {
     extern __shared__ u4 smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
     const int tile0 = blockIdx.x * NT;
-    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * 64);
+    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * MT * 64);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
     const TileStreams<NT> ts = tile_streams<NT>(w, tile0, tiles, N, G, lane);
-    const int xrow = min(r, M - 1);  // B columns r >= M: any valid row, their D columns are not stored
-    const h8* xl = reinterpret_cast<const h8*>(x + static_cast<int64_t>(xrow) * K + 32 * kb);
+    const int xrow = min(r, M - 1);  // B columns past M: any valid row, their D columns are not stored
+    const h8* xl[MT];
+#pragma unroll
+    for (int b = 0; b < MT; ++b)
+        xl[b] = reinterpret_cast<const h8*>(x + static_cast<int64_t>(min(16 * b + r, M - 1)) * K + 32 * kb);
     const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
     const int nch = (ge - gb + U - 1) / U;
 
@@ -359,60 +378,75 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         __syncthreads();
     }
 
-    f4 acc[NT];
+    f4 acc[NT][MT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
     for (; i + 2 < nch; i += 2) {
-        mma_chunk<true, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<true, XLDS, U, NT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<true, XLDS, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
     }
     if (i + 2 == nch) {
-        mma_chunk<true, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<false, XLDS, U, NT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XLDS, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
     } else if (i + 1 == nch) {
-        mma_chunk<false, XLDS, U, NT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
     }
     if (WK > 1) {
-        f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][64]
+        f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][MT][64]
         if (wave > 0) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) red[((wave - 1) * NT + t) * 64 + lane] = acc[t];
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int bb = 0; bb < MT; ++bb) red[(((wave - 1) * NT + t) * MT + bb) * 64 + lane] = acc[t][bb];
         }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int v = 0; v < WK - 1; ++v)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] += red[(v * NT + t) * 64 + lane];
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int bb = 0; bb < MT; ++bb) acc[t][bb] += red[((v * NT + t) * MT + bb) * 64 + lane];
     }
-    const int m = r;
     if (act) {  // N % 16 == 0 (checked on the host)
         const int half_n = N >> 1;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            f4 up;
-            up.x = __shfl_xor(acc[t].x, 32);
-            up.y = __shfl_xor(acc[t].y, 32);
-            up.z = __shfl_xor(acc[t].z, 32);
-            up.w = __shfl_xor(acc[t].w, 32);
             const int tt = tile0 + t;
-            if (kb >= 2 || m >= M || tt >= tiles) continue;
-            const int f = 8 * tt + 4 * kb;  // features f .. f + 3 of the [M, N/2] output
-            const h4 o = h4{static_cast<h1>(silu(acc[t].x) * up.x), static_cast<h1>(silu(acc[t].y) * up.y),
-                            static_cast<h1>(silu(acc[t].z) * up.z), static_cast<h1>(silu(acc[t].w) * up.w)};
-            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + f) = o;
+#pragma unroll
+            for (int bb = 0; bb < MT; ++bb) {
+                f4 up;
+                up.x = __shfl_xor(acc[t][bb].x, 32);
+                up.y = __shfl_xor(acc[t][bb].y, 32);
+                up.z = __shfl_xor(acc[t][bb].z, 32);
+                up.w = __shfl_xor(acc[t][bb].w, 32);
+                const int m = 16 * bb + r;
+                if (kb >= 2 || m >= M || tt >= tiles) continue;
+                const int f = 8 * tt + 4 * kb;  // features f .. f + 3 of the [M, N/2] output
+                const f4 g4 = acc[t][bb];
+                const h4 o = h4{static_cast<h1>(silu(g4.x) * up.x), static_cast<h1>(silu(g4.y) * up.y),
+                                static_cast<h1>(silu(g4.z) * up.z), static_cast<h1>(silu(g4.w) * up.w)};
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + f) = o;
+            }
         }
         return;
     }
-    if (m >= M) return;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int n = 16 * (tile0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
         if (n >= N) continue;
-        const h4 o = h4{static_cast<h1>(acc[t].x), static_cast<h1>(acc[t].y), static_cast<h1>(acc[t].z),
-                        static_cast<h1>(acc[t].w)};
-        *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) = o;
+#pragma unroll
+        for (int bb = 0; bb < MT; ++bb) {
+            const int m = 16 * bb + r;
+            if (m >= M) continue;
+            const f4 a4 = acc[t][bb];
+            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                h4{static_cast<h1>(a4.x), static_cast<h1>(a4.y), static_cast<h1>(a4.z), static_cast<h1>(a4.w)};
+        }
+    }
     }
 }
 
@@ -445,8 +479,10 @@ int decode_prepare(int dev) {
     if (rc == TW4_OK) rc = allow_lds(gemv_kernel<2, WK, U, T>);              \
     if (rc == TW4_OK) rc = allow_lds(gemv_kernel<3, WK, U, T>);              \
     if (rc == TW4_OK) rc = allow_lds(gemv_kernel<4, WK, U, T>);              \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, true>);            \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, false>);
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true>);         \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, false>);        \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, false>);        \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, false>);
     TW4_DECODE_CONFIGS(TW4_ATTR)
 #undef TW4_ATTR
     if (rc == TW4_OK) g_decode_ready[dev] = 1;
@@ -522,9 +558,12 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
                        uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, int act, void* stream) {
     int rc = check_operands("mma", x, packed, scales, zeros, y, M, N, K);
     if (rc) return rc;
-    TW4_REQUIRE(M >= 1 && M <= 16, TW4_EINVAL, "mma: 1 <= M <= 16 (M = %d)", M);
+    TW4_REQUIRE(M >= 1 && M <= 64, TW4_EINVAL, "mma: 1 <= M <= 64 (M = %d)", M);
     TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
                 "mma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    TW4_REQUIRE(mt == 1 || unroll * mt <= 4, TW4_ECONFIG,
+                "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
     rc = ensure_prepared();
     if (rc) return rc;
     auto xp = reinterpret_cast<const h1*>(x);
@@ -534,14 +573,19 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
     const int tiles = (N + 15) >> 4;
-    const bool xlds = static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+    const bool xlds = mt == 1 && static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
 #define TW4_MMA_CASE(WK, U, T)                                                                                \
     if (warps_k == WK && unroll == U && ntile == T) {                                                         \
-        const size_t lds = 16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * 64).total);     \
+        const size_t lds = 16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * mt * 64).total); \
+        const unsigned grid = (tiles + T - 1) / T;                                                            \
         if (xlds)                                                                                             \
-            mma_kernel<WK, U, T, true><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act); \
+            mma_kernel<WK, U, T, 1, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);     \
+        else if (mt == 1)                                                                                     \
+            mma_kernel<WK, U, T, 1, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
+        else if (mt == 2)                                                                                     \
+            mma_kernel<WK, U, T, 2, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
         else                                                                                                  \
-            mma_kernel<WK, U, T, false><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act); \
+            mma_kernel<WK, U, T, 4, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
         TW4_LAUNCH_CHECK("mma: launch");                                                                      \
         return TW4_OK;                                                                                        \
     }

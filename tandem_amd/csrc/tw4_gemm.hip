@@ -16,8 +16,9 @@
 //            4 kb + i of token r.
 //   WK = 2:  the two K wavefronts add their sums in LDS at the end.
 //   split-K: work units 0 .. dp - 1 are whole tiles; each later tile is shared by `splits` units
-//            that take contiguous ranges of K steps. A unit stores its fp32 partial tile to ws,
-//            then one agent-scope atomic on the tile's counter tells the last arriver, which adds
+//            that take contiguous ranges of K steps. A unit stores its fp32 partial tile to ws
+//            (agent-scope stores that write through the XCD's L2), then one agent-scope atomic on
+//            the tile's counter tells the last arriver, which adds
 //            the `splits` partials in split order (the result does not depend on arrival order),
 //            writes y and returns the counter to zero for the next call.
 //   act = 1: SwiGLU epilogue as in the decode kernel (gate rows 4 kb + i and up rows 8 + 4 kb + i
@@ -214,36 +215,46 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
     }
 
     if (nsplit > 1) {
-        constexpr int V = NT * MT * 64;  // f4 per wavefront partial
-        const int st = tile - dp;        // index among the split tiles
-        f4* wsv = reinterpret_cast<f4*>(ws);
+        // Partials and their reads are agent-scope relaxed atomics (global_store / global_load sc1:
+        // coherent across the XCDs' L2s without a cache-wide write-back or invalidate); each
+        // wavefront partial is stored [fragment][component][lane], so every instruction moves 256
+        // contiguous bytes. s_waitcnt vmcnt(0) + barrier order the stores before the count.
+        constexpr int V = NT * MT * 4 * 64;  // floats per wavefront partial
+        const int st = tile - dp;            // index among the split tiles
         if (wk == 0) {
-            f4* mine = wsv + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+            float* mine = ws + (static_cast<int64_t>(su) * WN + wn) * V + lane;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int b = 0; b < MT; ++b) mine[(t * MT + b) * 64] = acc[t][b];
+                for (int b = 0; b < MT; ++b)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        __hip_atomic_store(mine + ((t * MT + b) * 4 + c) * 64, acc[t][b][c], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
         }
-        __threadfence();  // release: the partial tile is visible device-wide before the count
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_flag = old == splits - 1;
         }
         __syncthreads();
         if (!last_flag) return;
-        __threadfence();  // acquire: every split's partial tile is visible
         if (wk == 0) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             for (int v = 0; v < splits; ++v) {
-                const f4* other = wsv + ((static_cast<int64_t>(st) * splits + v) * WN + wn) * V + lane;
+                const float* other = ws + ((static_cast<int64_t>(st) * splits + v) * WN + wn) * V + lane;
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int b = 0; b < MT; ++b) acc[t][b] += __builtin_nontemporal_load(other + (t * MT + b) * 64);
+                    for (int b = 0; b < MT; ++b)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            acc[t][b][c] += __hip_atomic_load(other + ((t * MT + b) * 4 + c) * 64, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

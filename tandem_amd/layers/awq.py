@@ -23,8 +23,8 @@ and w[k, n] = (q[k, n] - z[k // G, n]) * s[k // G, n].
 The nibble order inside a word is the reference's (python/tandem/layers/awq.py:12-20); the word
 order is this build's (the reference keeps each row contiguous: [N][K/G][4 j][4 cc]).
 
-Kernels (libtandem_w4.so): w4_gemv (M <= 4, vector ALUs), w4_mma (M <= 16, matrix cores) and
-w4_gemm (M > 16, matrix cores, LDS-staged activations, split-K). Where the table says so, with
+Kernels (libtandem_w4.so): w4_gemv (M <= 4, vector ALUs), w4_mma (M <= 64, matrix cores) and
+w4_gemm (any M, matrix cores, LDS-staged activations, split-K). Where the table says so, with
 TANDEM_W4_GEMM=0, with TANDEM_NO_CUDA_EXT=1 or for an unaligned x: HIP dequantize to float16 +
 torch.matmul (hipBLASLt).
 """
@@ -136,7 +136,7 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 
 # Decode kernel per GPU and (N, K, M), the fastest of bench_w4.py-style sweeps on the GPU:
 #   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4
-#   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 16
+#   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
 # iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
 # (Same dispatch structure as python/tandem/layers/awq.py:136-160.)
@@ -150,12 +150,14 @@ W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
 # GEMM for M > 16 per GPU and (N, K) / (N, K, "silu"): ((m_max, config), ...) by increasing m_max;
 # M past the last m_max uses the last entry. config = (MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS) of
 # w4_gemm (BM = 16 MT tokens, each wavefront 16 NT rows, WARPS_N x WARPS_K wavefronts, STAGES-deep
-# LDS ring, SPLITS: split-K of every tile, or 0: of the last, partial wave of tiles only), or None:
-# dequantize to float16 + torch.matmul. Shapes without an entry use DEFAULT_GEMM.
+# LDS ring, SPLITS: split-K of every tile, or 0: of the last, partial wave of tiles only), or
+# ("mma", warps_k, unroll, ntile): the streaming matrix-core kernel of the decode path, whose 16-token
+# batch tiles cover M <= 64 (bandwidth-bound batches), or None: dequantize to float16 +
+# torch.matmul. Shapes without an entry use DEFAULT_GEMM.
 # TANDEM_W4_GEMM=0: always dequantize + torch.matmul (python/tandem/layers/awq.py:163-186).
 W4Gemm = tuple
 DEFAULT_GEMM: tuple[tuple[int, W4Gemm | None], ...] = (
-    (32, (2, 1, 4, 1, 2, 0)), (64, (4, 1, 4, 1, 2, 0)), (1 << 30, (8, 2, 4, 1, 2, 0)))
+    (64, ("mma", 8, 1, 1)), (1 << 30, (8, 2, 4, 1, 2, 0)))
 W4_GEMM_KERNELS: dict[str, dict[tuple, tuple[tuple[int, W4Gemm | None], ...]]] = {
     MI355X: {},
 }
@@ -263,7 +265,9 @@ class W4Linear(nn.Module):
             if ext is not None:
                 key = (self.out_features, self.in_features) + (("silu",) if self.silu_mul else ())
                 cfg = pick_gemm(self.gemm_kernels.get(key, DEFAULT_GEMM), x.shape[0])
-                if cfg is not None:
+                if cfg is not None and cfg[0] == "mma" and x.shape[0] <= 64:  # the streaming kernel, M <= 64
+                    return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg[1:], int(self.silu_mul))
+                if cfg is not None and cfg[0] != "mma":
                     buf, locks = w4_hip.workspace(x.device)
                     return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
         return self._dense(x)

@@ -156,8 +156,8 @@ class W4Extension:
 
     def w4_mma(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int) -> torch.Tensor:
         m, n, k = check_operands("w4_mma", x, w, s, z)
-        if not 1 <= m <= 16:
-            raise RuntimeError("w4_mma: M <= 16")
+        if not 1 <= m <= 64:
+            raise RuntimeError("w4_mma: M <= 64 (16-token batch tiles: 1, 2 or 4)")
         if act not in (0, 1) or (act and n % 16):
             raise RuntimeError("w4_mma: act 0, or 1 (SwiGLU) with N % 16 == 0")
         y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)

@@ -103,9 +103,12 @@ def main(argv=None) -> int:
                     except RuntimeError:
                         continue
                     res[("gemv", *cfg)] = us
-            if "mma" in kinds and m <= 16:
+            if "mma" in kinds and m <= 64:
                 for cfg in w4_hip.decode_configs():
-                    us = time_us([lambda w=w, c=cfg: ext.w4_mma(x, *w, *c, act) for w in ws], stream)
+                    try:
+                        us = time_us([lambda w=w, c=cfg: ext.w4_mma(x, *w, *c, act) for w in ws], stream)
+                    except RuntimeError:  # unroll * batch tiles above 4
+                        continue
                     res[("mma", *cfg)] = us
             if "gemm" in kinds:
                 g = k // 128

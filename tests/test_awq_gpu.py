@@ -125,6 +125,42 @@ def test_mma_every_config(ext):
                 check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg))
 
 
+def _wide_ok(cfg, m) -> bool:
+    mt = 1 if m <= 16 else 2 if m <= 32 else 4
+    return mt == 1 or cfg[1] * mt <= 4
+
+
+def test_mma_wide_batches(ext):
+    """The streaming matrix-core kernel with 2 or 4 batch tiles (M 17 .. 64), every compiled config
+    it accepts; the rest are refused with an error, never launched."""
+    for k, n in SHAPES:
+        c = Case(k, n, seed=14)
+        for m in (17, 32, 33, 50, 64):
+            x = c.x(m, seed=600 + m)
+            ref = o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                if not _wide_ok(cfg, m):
+                    with pytest.raises(RuntimeError):
+                        ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0)
+                    continue
+                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg))
+
+
+def test_mma_wide_silu_mul(ext):
+    for k, n in ((128, 32), (4096, 1024)):
+        c = Case(k, n, seed=15, interleave=True)
+        for m in (24, 40, 64):
+            x = c.x(m, seed=700 + m)
+            ref = o.swiglu_reference(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                if _wide_ok(cfg, m):
+                    y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
+                    assert y.shape == (m, n // 2)
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg))
+
+
 def test_mma_silu_mul(ext):
     """SwiGLU epilogue (act = 1) on interleaved rows: y = silu(gate) * up (tests/test_awq.py:302-314)."""
     for k, n in ((128, 32), (1024, 512), (4096, 1024)):
@@ -285,7 +321,7 @@ def test_w4linear_small_and_large_batch():
         xn = rng.standard_normal((m, k)).astype(np.float16)
         xu.copy_(gpu(xn))
         check_close(layer(xu), o.linear(xn, c.w_exact), 0.05, 0.02, ("unaligned", m))
-    for cfg in ((2, 2, 4, 2, 2, 2), (4, 2, 4, 1, 2, 0), None):
+    for cfg in ((2, 2, 4, 2, 2, 2), (4, 2, 4, 1, 2, 0), ("mma", 8, 1, 1), None):
         layer.gemm_kernels = {(n, k): ((1 << 30, cfg),)}
         x = rng.standard_normal((50, k)).astype(np.float16)
         check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, cfg)

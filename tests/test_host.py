@@ -44,7 +44,11 @@ def test_config_queries():
     assert len(dec) >= 8 and all(len(c) == 3 and c[0] >= 1 and c[1] >= 1 for c in dec)
     assert len(gemm) >= 8 and all(len(c) == 5 and c[3] in (1, 2) for c in gemm)
     assert awq.DEFAULT_KERNEL[1:] in dec
-    assert all(cfg[:5] in gemm for _, cfg in awq.DEFAULT_GEMM if cfg is not None)
+    for m_max, cfg in awq.DEFAULT_GEMM:
+        if cfg is not None and cfg[0] == "mma":
+            assert tuple(cfg[1:]) in dec and m_max <= 64
+        elif cfg is not None:
+            assert cfg[:5] in gemm
 
 
 def test_library_identity():
@@ -70,7 +74,7 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_repack_awq(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 128, 24, 1, None), "interleave"),
         (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 5, 64, 128, 4, 2, 1, None), "M <= 4"),
         (lambda: lib.tw4_gemv(_fake(4100), _fake(), _fake(), _fake(), _fake(), 1, 64, 128, 4, 2, 1, None), "aligned"),
-        (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 17, 64, 128, 4, 2, 1, 0, None), "M <= 16"),
+        (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 65, 64, 128, 4, 2, 1, 0, None), "M <= 64"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
                               32, 64, 128, 2, 1, 4, 1, 2, 17, 0, None), "splits"),
@@ -200,7 +204,7 @@ def test_tables_are_well_formed():
         m_maxes = [m for m, _ in ladder]
         assert m_maxes == sorted(m_maxes)
         for _, cfg in ladder:
-            assert cfg is None or len(cfg) == 6
+            assert cfg is None or len(cfg) == 6 or (cfg[0] == "mma" and len(cfg) == 4)
 
 
 def test_make_linear_and_finalize_quantized():
