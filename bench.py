@@ -102,15 +102,18 @@ def time_graph(torch, graph, stream, reps: int) -> float:
 
 
 def kernel_of(awq, lin, m: int) -> str:
-    """Which kernel W4Linear.forward runs for M (the same lookup as the forward)."""
-    key = (lin.out_features, lin.in_features, m)
+    """Which kernel W4Linear.forward runs for M (the same lookups as the forward)."""
     if m <= 16:
-        if lin.silu_mul:
-            return "mma"
-        kind = lin.kernels.get(key, awq.DEFAULT_KERNEL)
+        key = (lin.out_features, lin.in_features, m)
+        kind = (lin.kernels.get((*key, "silu")) if lin.silu_mul else None) or lin.kernels.get(key, awq.DEFAULT_KERNEL)
+        if kind[0] == "gemv" and (m > 4 or lin.silu_mul):
+            kind = awq.DEFAULT_KERNEL
         return f"{kind[0]}{tuple(kind[1:])}"
-    cfg = awq.pick_gemm(lin.gemm_kernels.get((lin.out_features, lin.in_features), awq.DEFAULT_GEMM), m)
-    return f"gemm{cfg}" if cfg is not None and awq.FUSED_GEMM else "dequant+matmul"
+    key = (lin.out_features, lin.in_features) + (("silu",) if lin.silu_mul else ())
+    cfg = awq.pick_gemm(lin.gemm_kernels.get(key, awq.DEFAULT_GEMM), m)
+    if cfg is None or not awq.FUSED_GEMM:
+        return "dequant+matmul"
+    return f"mma{tuple(cfg[1:])}" if cfg[0] == "mma" else f"gemm{cfg}"
 
 
 def cpu_baseline(budget_s: float, m: int) -> dict:

@@ -38,6 +38,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from tandem_amd.layers import w4_hip
+from tandem_amd.layers.w4_tables import GFX950_DECODE, GFX950_GEMM
 
 # AWQ packs output columns j = 0..7 of an int32 in nibble order [0, 2, 4, 6, 1, 3, 5, 7]: column j
 # lives in nibble REVERSE[j] (python/tandem/layers/awq.py:38-39)
@@ -134,17 +135,23 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
     return w if dtype == torch.float16 else w.to(dtype)
 
 
-# Decode kernel per GPU and (N, K, M), the fastest of bench_w4.py-style sweeps on the GPU:
-#   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4
+# Decode kernel per GPU and (N, K, M) / (N, K, M, "silu") for M <= 16, the fastest of
+# `python -m tandem_amd.tune` sweeps on the GPU:
+#   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4, no SwiGLU epilogue
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
+#   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
 # iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
-# (Same dispatch structure as python/tandem/layers/awq.py:136-160.)
+# Tables are keyed by device name and by gfx architecture; finalize() tries the name it is given,
+# then the architecture of the layer's GPU. (Same dispatch structure as
+# python/tandem/layers/awq.py:136-160.)
 W4Kernel = tuple
 DEFAULT_KERNEL: W4Kernel = ("mma", 4, 2, 1)
 MI355X = "AMD Instinct MI355X"
+GFX950 = "gfx950"
 W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
-    MI355X: {},
+    MI355X: GFX950_DECODE,
+    GFX950: GFX950_DECODE,
 }
 
 # GEMM for M > 16 per GPU and (N, K) / (N, K, "silu"): ((m_max, config), ...) by increasing m_max;
@@ -157,9 +164,10 @@ W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
 # TANDEM_W4_GEMM=0: always dequantize + torch.matmul (python/tandem/layers/awq.py:163-186).
 W4Gemm = tuple
 DEFAULT_GEMM: tuple[tuple[int, W4Gemm | None], ...] = (
-    (64, ("mma", 8, 1, 1)), (1 << 30, (8, 2, 4, 1, 2, 0)))
+    (64, ("mma", 8, 1, 1)), (1 << 30, (4, 2, 4, 1, 2, 0)))
 W4_GEMM_KERNELS: dict[str, dict[tuple, tuple[tuple[int, W4Gemm | None], ...]]] = {
-    MI355X: {},
+    MI355X: GFX950_GEMM,
+    GFX950: GFX950_GEMM,
 }
 FUSED_GEMM = os.environ.get("TANDEM_W4_GEMM", "1") != "0"
 
@@ -184,6 +192,21 @@ def _hip_ok(x: torch.Tensor) -> bool:
 def _gemm_ok(x: torch.Tensor) -> bool:
     """The M > 16 GEMM (python/tandem/layers/awq.py:201-203)."""
     return FUSED_GEMM and x.is_cuda and _aligned(x) and x.shape[0] > 16
+
+
+def _table(tables: dict, device_name: str | None, device: torch.device) -> dict:
+    """None: no table, every shape takes the defaults (python/tandem/layers/awq.py:244-245).
+    Else the table for `device_name`, or for the gfx architecture of `device` when the name is not
+    a key: a HIP runtime may report a generic marketing name ("AMD Radeon Graphics") or, under
+    rocprofv3, an empty one."""
+    if device_name is None:
+        return {}
+    if device_name in tables:
+        return tables[device_name]
+    if device.type == "cuda" and torch.cuda.is_available():
+        arch = getattr(torch.cuda.get_device_properties(device), "gcnArchName", "").split(":")[0]
+        return tables.get(arch, {})
+    return {}
 
 
 class W4Linear(nn.Module):
@@ -224,8 +247,8 @@ class W4Linear(nn.Module):
         self.register_buffer("scales", scales)
         self.register_buffer("zeros", zeros)
         self.awq_layout = False
-        self.kernels = W4_KERNELS.get(device_name, {}) if device_name else {}
-        self.gemm_kernels = W4_GEMM_KERNELS.get(device_name, {}) if device_name else {}
+        self.kernels = _table(W4_KERNELS, device_name, packed.device)
+        self.gemm_kernels = _table(W4_GEMM_KERNELS, device_name, packed.device)
         # device set-up and the split-K workspace now, not inside graph capture
         if w4_hip.load() is not None:
             w4_hip.workspace(packed.device)
@@ -239,27 +262,30 @@ class W4Linear(nn.Module):
         y = F.linear(x, w)
         return silu_and_mul(y) if self.silu_mul else y
 
+    def _gemm(self, ext, x: torch.Tensor, cfg) -> torch.Tensor:
+        buf, locks = w4_hip.workspace(x.device)
+        return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.awq_layout:
             raise RuntimeError("W4Linear: call finalize() (after moving the layer to the GPU) before forward")
         if x.dim() == 2 and x.shape[0] == 0:
             return x.new_empty((0, self.out_features // 2 if self.silu_mul else self.out_features))
-        if _hip_ok(x):
+        if _hip_ok(x):  # 1 <= M <= 16: the (N, K, M) table
             ext = w4_hip.load()
             if ext is not None:
                 m = x.shape[0]
                 key = (self.out_features, self.in_features, m)
-                if self.silu_mul:  # matrix-core kernel only (the epilogue pairs lanes l and l + 32)
-                    kind, *cfg = self.kernels.get((*key, "silu")) or self.kernels.get(key, DEFAULT_KERNEL)
-                    if kind != "mma":
-                        _, *cfg = DEFAULT_KERNEL
-                    return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, 1)
-                kind, *cfg = self.kernels.get(key, DEFAULT_KERNEL)
-                if kind == "gemv" and m <= 4:
+                entry = (self.kernels.get((*key, "silu")) if self.silu_mul else None) or \
+                    self.kernels.get(key, DEFAULT_KERNEL)
+                kind, *cfg = entry
+                if kind == "gemm":
+                    return self._gemm(ext, x, cfg)
+                if kind == "gemv" and m <= 4 and not self.silu_mul:
                     return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg)
-                if kind != "mma":
+                if kind != "mma":  # gemv past M = 4, or with the SwiGLU epilogue
                     _, *cfg = DEFAULT_KERNEL
-                return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, 0)
+                return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
         elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul
             ext = w4_hip.load()
             if ext is not None:
@@ -268,6 +294,5 @@ class W4Linear(nn.Module):
                 if cfg is not None and cfg[0] == "mma" and x.shape[0] <= 64:  # the streaming kernel, M <= 64
                     return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg[1:], int(self.silu_mul))
                 if cfg is not None and cfg[0] != "mma":
-                    buf, locks = w4_hip.workspace(x.device)
-                    return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
+                    return self._gemm(ext, x, cfg)
         return self._dense(x)

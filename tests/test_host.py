@@ -195,16 +195,25 @@ def test_pick_gemm_ladder():
 
 
 def test_tables_are_well_formed():
-    kinds = {"gemv", "mma"}
-    assert awq.DEFAULT_KERNEL[0] in kinds and len(awq.DEFAULT_KERNEL) == 4
+    assert awq.DEFAULT_KERNEL[0] in ("gemv", "mma") and len(awq.DEFAULT_KERNEL) == 4
+    decode = set(w4_hip.decode_configs())
+    gemm = set(w4_hip.gemm_configs())
     for table in awq.W4_KERNELS.values():
         for key, cfg in table.items():
-            assert cfg[0] in kinds and len(cfg) == 4 and len(key) in (3, 4)
+            assert len(key) == 3 or (len(key) == 4 and key[3] == "silu")
+            n, k, m = key[:3]
+            assert 1 <= m <= 16 and k % 128 == 0 and n % 8 == 0
+            if cfg[0] == "gemm":  # a compiled GEMM config and a split mode
+                assert len(cfg) == 7 and tuple(cfg[1:6]) in gemm and 0 <= cfg[6] <= 16
+            else:  # a compiled decode config; gemv only where it runs (M <= 4, no epilogue)
+                assert cfg[0] in ("gemv", "mma") and tuple(cfg[1:]) in decode
+                assert cfg[0] == "mma" or (m <= 4 and len(key) == 3)
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
         m_maxes = [m for m, _ in ladder]
         assert m_maxes == sorted(m_maxes)
-        for _, cfg in ladder:
-            assert cfg is None or len(cfg) == 6 or (cfg[0] == "mma" and len(cfg) == 4)
+        for m_max, cfg in ladder:
+            assert cfg is None or (len(cfg) == 6 and tuple(cfg[:5]) in gemm) or \
+                (cfg[0] == "mma" and tuple(cfg[1:]) in decode and m_max <= 64 and cfg[2] * -(-m_max // 16) <= 4)
 
 
 def test_make_linear_and_finalize_quantized():
