@@ -88,8 +88,9 @@ int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              int warps_k, int unroll, int ntile, void* stream);
 
 /* Decode on the matrix cores (v_mfma_f32_16x16x32_f16, weights as the A operand, the batch on
- * the 16-column side, ceil(M / 16) column tiles), 1 <= M <= 64. act = 1: y = silu(gate) * up, [M, N/2], rows in
- * interleave_gate_up order (N % 16 == 0); act = 0: y [M, N].
+ * the 16-column side, ceil(M / 16) column tiles), 1 <= M <= 64; unroll * ceil(M / 16) <= 4.
+ * act = 1: y = silu(gate) * up, [M, N/2], rows in interleave_gate_up order (N % 16 == 0);
+ * act = 0: y [M, N].
  * Replaces w4_mma (python/tandem/csrc/w4_gemv.cu:166-295, 619-648). */
 int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
             const uint16_t* zeros, uint16_t* y, int M, int N, int K,
