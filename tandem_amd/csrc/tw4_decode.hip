@@ -10,9 +10,9 @@
 // computed. Loads retire in issue order, so a chunk issues what it needs now first, then the
 // prefetch, and no branch sits around a load: every wait is exact.
 //
-// x is copied to LDS once per workgroup, while the first chunk is in flight, when it fits (row
-// stride K + 8 halves, so the 16 rows of a B-fragment read hit 16 different bank groups); the WK
-// partial sums are added in LDS at the end.
+// x goes to LDS when it fits (row stride K + 8 halves, so the 16 rows of a B-fragment read hit 16
+// different bank groups): each wavefront stages only its own groups' slice, while its first chunk
+// is in flight, with no workgroup barrier. The WK partial sums are added in LDS at the end.
 //
 //   gemv: vector ALUs, M <= 4, x always in LDS, stored as x' (pairs 2, 3 and 6, 7 of every 8 k
 //         divided by 16) with per-slice sums of x' and x (fill_x_biased). A word becomes four
@@ -116,49 +116,99 @@ __device__ __forceinline__ void load_chunk(WeightSet<U, NT>& ws, const TileStrea
     }
 }
 
-// x [M, K] -> LDS rows of K + 8 halves. Coalesced: consecutive threads read consecutive 16 bytes.
-__device__ __forceinline__ void fill_x(u4* smem, const DecodeLds& l, const h1* __restrict__ x, int M, int K,
-                                       int threads) {
-    const int kx = K >> 3;
-    const u4* xg = reinterpret_cast<const u4*>(x);
-    for (int c = threadIdx.x; c < M * kx; c += threads) {
-        const int row = c / kx;
-        smem[row * l.xs + (c - row * kx)] = xg[c];
-    }
+// Per-wavefront x staging. A wavefront reads x only over its own quant groups [gb, ge), so it stages
+// just that slice of every row into the workgroup's LDS image of x (rows of K + 8 halves) and needs
+// no workgroup barrier: its lanes write, then read, their own slice. The slice is M rows of n16
+// chunks of 16 bytes (from column c0), walked as one flat index f = m n16 + c: lane l takes chunks
+// l, l + 64, ... in batches of kXB, all of a batch's loads before its stores. Chunks past the end
+// repeat the last one (identical duplicate writes), so no branch sits around a load or a store. The
+// first batch is loaded before the first weight chunk is issued, so waiting for it never waits for
+// the weights (loads retire in order).
+constexpr int kXB = 2;
+
+struct XSlice {
+    int c0;          // first chunk column: 16 gb
+    int n16;         // chunks per row: 16 (ge - gb), a multiple of 4
+    int n;           // M n16
+    uint32_t magic;  // ceil(2^32 / n16): f / n16 == umulhi(f, magic) for f < 16 n16 <= 2^17 (K <= 65536)
+};
+
+__device__ __forceinline__ XSlice x_slice(int gb, int ge, int M) {
+    const int n16 = 16 * (ge - gb);
+    return XSlice{16 * gb, n16, M * n16, n16 > 0 ? static_cast<uint32_t>(0xFFFFFFFFu / static_cast<uint32_t>(n16)) + 1u : 0u};
 }
 
-// x [M, K] -> LDS rows of K + 8 halves with every pair k = 8 j + 2, 3 and 8 j + 6, 7 divided by
-// 16 (x', exact: a power-of-two scale, rounded only where x / 16 is below fp16's normal range),
-// plus, per (m, group, 32-k slice kb), the float sums A = sum x' and B = sum x of the slice
-// (corr[(m G + g) 4 + kb], float2). A word's four magic halves (1024 + q for weights 8 j + 0, 1 and
-// 8 j + 4, 5; 1024 + 16 q for 8 j + 2, 3 and 8 j + 6, 7) dotted with x' give
-// sum q x + 1024 sum x', so sum (q - z) x = dot - 1024 A - z B.
-__device__ __forceinline__ void fill_x_biased(u4* smem, const DecodeLds& l, float2* corr, const h1* __restrict__ x,
-                                              int M, int K, int threads) {
-    const int kx = K >> 3;
-    const u4* xg = reinterpret_cast<const u4*>(x);
-    const h2 lo = h2{static_cast<h1>(1.0f), static_cast<h1>(1.0f)};
-    const h2 hi = h2{static_cast<h1>(0.0625f), static_cast<h1>(0.0625f)};
-    for (int c = threadIdx.x; c < M * kx; c += threads) {  // M kx and threads are multiples of 4
-        const int row = c / kx, col = c - row * kx;
-        const u4 v = xg[c];
+struct XPos {
+    int m, c;
+};
+
+// Flat chunk f -> (row, chunk in row); f past the slice -> its last chunk.
+__device__ __forceinline__ XPos x_pos(const XSlice& xs, int f) {
+    f = min(f, xs.n - 1);
+    const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(f), xs.magic));
+    return XPos{m, f - m * xs.n16};
+}
+
+__device__ __forceinline__ u4 x_chunk(const u4* xg, int kx, const XSlice& xs, XPos p) {
+    return xg[static_cast<int64_t>(p.m) * kx + xs.c0 + p.c];
+}
+
+__device__ __forceinline__ void load_x_batch(u4 (&v)[kXB], const u4* xg, int kx, const XSlice& xs, int f0) {
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) v[j] = x_chunk(xg, kx, xs, x_pos(xs, f0 + 64 * j));
+}
+
+// Flat chunk f into LDS. BIASED: as x' (pairs k = 8 j + 2, 3 and 8 j + 6, 7 divided by 16: exact, a
+// power-of-two scale, rounded only where x / 16 is below fp16's normal range) plus, per (m, group,
+// 32-k slice kb), the float sums A = sum x' and B = sum x of the slice (corr[(m G + g) 4 + kb],
+// float2). A word's four magic halves (1024 + q for weights 8 j + 0, 1 and 8 j + 4, 5; 1024 + 16 q
+// for 8 j + 2, 3 and 8 j + 6, 7) dotted with x' give sum q x + 1024 sum x', so
+// sum (q - z) x = dot - 1024 A - z B. The four chunks of a 32-k slice are lanes 4 i .. 4 i + 3 of
+// one call (n16 and the lane offsets are multiples of 4); past the slice end all four or none.
+template <bool BIASED>
+__device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, float2* corr, int kx, const XSlice& xs,
+                                              u4 v, int f) {
+    const XPos p = x_pos(xs, f);
+    const int col = xs.c0 + p.c;
+    if constexpr (!BIASED) {
+        smem[p.m * l.xs + col] = v;
+    } else {
+        const h2 lo = h2{static_cast<h1>(1.0f), static_cast<h1>(1.0f)};
+        const h2 hi = h2{static_cast<h1>(0.0625f), static_cast<h1>(0.0625f)};
         const h2 x0 = bitcast<h2>(v.x), x1 = bitcast<h2>(v.y), x2 = bitcast<h2>(v.z), x3 = bitcast<h2>(v.w);
         const h2 y0 = x0 * lo, y1 = x1 * hi, y2 = x2 * lo, y3 = x3 * hi;
-        smem[row * l.xs + col] = u4{bitcast<uint32_t>(y0), bitcast<uint32_t>(y1), bitcast<uint32_t>(y2),
-                                    bitcast<uint32_t>(y3)};
         float a = static_cast<float>(y0.x) + static_cast<float>(y0.y) + static_cast<float>(y1.x) +
                   static_cast<float>(y1.y) + static_cast<float>(y2.x) + static_cast<float>(y2.y) +
                   static_cast<float>(y3.x) + static_cast<float>(y3.y);
         float b = static_cast<float>(x0.x) + static_cast<float>(x0.y) + static_cast<float>(x1.x) +
                   static_cast<float>(x1.y) + static_cast<float>(x2.x) + static_cast<float>(x2.y) +
                   static_cast<float>(x3.x) + static_cast<float>(x3.y);
-        // the four 16-byte chunks of a 32-k slice are lanes 4 i .. 4 i + 3 of this iteration
         a += __shfl_xor(a, 1);
         b += __shfl_xor(b, 1);
         a += __shfl_xor(a, 2);
         b += __shfl_xor(b, 2);
-        if ((col & 3) == 0) corr[row * (kx >> 2) + (col >> 2)] = float2{a, b};
+        smem[p.m * l.xs + col] =
+            u4{bitcast<uint32_t>(y0), bitcast<uint32_t>(y1), bitcast<uint32_t>(y2), bitcast<uint32_t>(y3)};
+        if ((col & 3) == 0 && f < xs.n) corr[p.m * (kx >> 2) + (col >> 2)] = float2{a, b};
     }
+}
+
+// Stores the first batch (already loaded), then loads and stores the rest of the slice batch by
+// batch; ends with the wavefront's LDS writes ordered before its reads.
+template <bool BIASED>
+__device__ __forceinline__ void stage_x(u4* smem, const DecodeLds& l, float2* corr, const u4* xg, int kx,
+                                        const XSlice& xs, const u4 (&first)[kXB], int lane) {
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED>(smem, l, corr, kx, xs, first[j], lane + 64 * j);
+    for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {  // wavefront-uniform trip count
+        u4 v[kXB];
+        load_x_batch(v, xg, kx, xs, f0);
+#pragma unroll
+        for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED>(smem, l, corr, kx, xs, v[j], f0 + 64 * j);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ __forceinline__ GroupQ group_q_raw(uint32_t s, uint32_t z, bool valid) {
@@ -236,10 +286,18 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const int nch = (ge - gb + U - 1) / U;
     float2* corr = reinterpret_cast<float2*>(smem + l.corr);
 
+    const int kx = K >> 3;
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    const XSlice xsl = x_slice(gb, ge, M);
     WeightSet<U, NT> a, b;
-    if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
-    fill_x_biased(smem, l, corr, x, M, K, WK * 64);
-    __syncthreads();
+    if (nch > 0) {
+        u4 xfirst[kXB];
+        load_x_batch(xfirst, xg, kx, xsl, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_x<true>(smem, l, corr, xg, kx, xsl, xfirst, lane);
+    }
 
     float acc[NT][M];
 #pragma unroll
@@ -372,10 +430,20 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int nch = (ge - gb + U - 1) / U;
 
     WeightSet<U, NT> a, b;
-    if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
     if constexpr (XLDS) {
-        fill_x(smem, l, x, M, K, WK * 64);
-        __syncthreads();
+        const int kx = K >> 3;
+        const u4* xg = reinterpret_cast<const u4*>(x);
+        const XSlice xsl = x_slice(gb, ge, M);
+        if (nch > 0) {
+            u4 xfirst[kXB];
+            load_x_batch(xfirst, xg, kx, xsl, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            stage_x<false>(smem, l, nullptr, xg, kx, xsl, xfirst, lane);
+        }
+    } else {
+        if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
     }
 
     f4 acc[NT][MT];
@@ -538,6 +606,7 @@ extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t
     int rc = check_operands("gemv", x, packed, scales, zeros, y, M, N, K);
     if (rc) return rc;
     TW4_REQUIRE(M >= 1 && M <= 4, TW4_EINVAL, "gemv: 1 <= M <= 4 (M = %d; larger M: mma)", M);
+    TW4_REQUIRE(K <= 65536, TW4_EINVAL, "gemv: K <= 65536 (K = %d; larger K: mma)", K);
     rc = ensure_prepared();
     if (rc) return rc;
     auto xp = reinterpret_cast<const h1*>(x);

@@ -74,6 +74,7 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_repack_awq(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 128, 24, 1, None), "interleave"),
         (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 5, 64, 128, 4, 2, 1, None), "M <= 4"),
         (lambda: lib.tw4_gemv(_fake(4100), _fake(), _fake(), _fake(), _fake(), 1, 64, 128, 4, 2, 1, None), "aligned"),
+        (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 64, 65536 + 128, 1, 4, 1, None), "K <= 65536"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 65, 64, 128, 4, 2, 1, 0, None), "M <= 64"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
