@@ -37,10 +37,19 @@
 namespace tw4 {
 
 template <int U, int NT>
-struct WeightSet {  // one chunk's weight blocks, scales and zeros, per lane
+struct WeightSet {  // one chunk's weight blocks and group parameters, per lane
     u4 w[U][NT];
-    uint32_t s[U][NT], z[U][NT];
+    uint32_t p[U][NT];  // the row's scale (lanes of rows kb = 0, 2) or zero (kb = 1, 3): see scale_zero
 };
+
+// Lanes 16 kb + r of even kb load row r's scale, of odd kb its zero: one 2-byte load per lane and
+// group instead of two. v_permlane16_swap exchanges rows 0 <-> 1 and 2 <-> 3 of two copies, which
+// leaves the even rows' values (scales) in the first result and the odd rows' (zeros) in the second.
+__device__ __forceinline__ void scale_zero(uint32_t p, uint32_t& s, uint32_t& z) {
+    const auto sz = __builtin_amdgcn_permlane16_swap(p, p, false, false);
+    s = sz[0];
+    z = sz[1];
+}
 
 // The workgroup's row tiles. Everything but `lane` and `prow` is uniform across the wavefront (the
 // tile index comes from blockIdx), so tile and group offsets stay in scalar registers and each
@@ -52,13 +61,16 @@ struct TileStreams {
     int rows[NT];        // rows of the tile: the scale / zero stride between groups
     int prow[NT];        // this lane's row in the tile (clamped: padding rows have zero weights)
     int lane;
+    const uint16_t* pb;  // scales (even kb) or zeros (odd kb)
 };
 
 template <int NT>
-__device__ __forceinline__ TileStreams<NT> tile_streams(const u4* w, int tile0, int tiles, int N, int G, int lane) {
+__device__ __forceinline__ TileStreams<NT> tile_streams(const u4* w, const uint16_t* s16, const uint16_t* z16, int tile0,
+                                                       int tiles, int N, int G, int lane) {
     TileStreams<NT> ts;
     const int r = lane & 15;
     ts.lane = lane;
+    ts.pb = (lane & 16) ? z16 : s16;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int tt = min(tile0 + t, tiles - 1);  // tiles past the end recompute the last one; not stored
@@ -110,8 +122,7 @@ __device__ __forceinline__ void load_chunk(WeightSet<U, NT>& ws, const TileStrea
         for (int t = 0; t < NT; ++t) {
             ws.w[u][t] = load_stream(ts.w[t] + static_cast<int64_t>(g) * kBlockU4 + ts.lane);
             const int64_t pg = ts.p[t] + static_cast<int64_t>(g) * ts.rows[t];
-            ws.s[u][t] = (s16 + pg)[ts.prow[t]];
-            ws.z[u][t] = (z16 + pg)[ts.prow[t]];
+            ws.p[u][t] = (ts.pb + pg)[ts.prow[t]];
         }
     }
 }
@@ -259,8 +270,10 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
             const float2 c = corr[(m * G + g) * 4 + kb];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const float sc = valid ? static_cast<float>(as_h1(cur.s[u][t])) : 0.0f;
-                const float zf = static_cast<float>(as_h1(cur.z[u][t]));
+                uint32_t s_raw, z_raw;
+                scale_zero(cur.p[u][t], s_raw, z_raw);
+                const float sc = valid ? static_cast<float>(as_h1(s_raw)) : 0.0f;
+                const float zf = static_cast<float>(as_h1(z_raw));
                 const float v = __builtin_fmaf(-zf, c.y, __builtin_fmaf(-1024.0f, c.x, part[t][m]));
                 acc[t][m] = __builtin_fmaf(v, sc, acc[t][m]);
             }
@@ -281,7 +294,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
-    const TileStreams<NT> ts = tile_streams<NT>(w, tile0, tiles, N, G, lane);
+    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
     const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
     const int nch = (ge - gb + U - 1) / U;
     float2* corr = reinterpret_cast<float2*>(smem + l.corr);
@@ -382,7 +395,11 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
         const int g = min(graw, ge - 1);
         GroupQ p[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) p[t] = group_q_raw(cur.s[u][t], cur.z[u][t], valid);
+        for (int t = 0; t < NT; ++t) {
+            uint32_t s_raw, z_raw;
+            scale_zero(cur.p[u][t], s_raw, z_raw);
+            p[t] = group_q_raw(s_raw, z_raw, valid);
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             h8 xv[MT];
@@ -420,7 +437,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
-    const TileStreams<NT> ts = tile_streams<NT>(w, tile0, tiles, N, G, lane);
+    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
     const int xrow = min(r, M - 1);  // B columns past M: any valid row, their D columns are not stored
     const h8* xl[MT];
 #pragma unroll
