@@ -102,6 +102,31 @@ __device__ __forceinline__ u4 load_stream(const u4* p) {  // weights: read once,
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
+// Cross-lane exchanges on the VALU (DPP and gfx950's permlane swaps) instead of the LDS crossbar.
+// DPP quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]: the value of lane l ^ 1 and of lane l ^ 2.
+__device__ __forceinline__ float lane_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// v_permlane16_swap / v_permlane32_swap on two copies of v leave rows {0, 2} / {1, 3} (resp. the
+// lower / upper 32 lanes) of v in every lane of the first / second result. Sum of lanes r, r + 16,
+// r + 32, r + 48 in every lane, added as (v0 + v1) + (v2 + v3).
+__device__ __forceinline__ float sum_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// The value of lane l ^ 32.
+__device__ __forceinline__ float lane_xor32(float v, int lane) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(lane < 32 ? a[1] : a[0]);
+}
+
 __device__ __forceinline__ f4 mfma16x16x32(const h8& a, const h8& b, const f4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

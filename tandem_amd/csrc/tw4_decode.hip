@@ -153,9 +153,12 @@ struct XPos {
     int m, c;
 };
 
-// Flat chunk f -> (row, chunk in row); f past the slice -> its last chunk.
+// Flat chunk f -> (row, chunk in row); f past the slice -> its last chunk. ONE_ROW: M == 1 known at
+// compile time, no division.
+template <bool ONE_ROW>
 __device__ __forceinline__ XPos x_pos(const XSlice& xs, int f) {
     f = min(f, xs.n - 1);
+    if constexpr (ONE_ROW) return XPos{0, f};
     const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(f), xs.magic));
     return XPos{m, f - m * xs.n16};
 }
@@ -164,9 +167,10 @@ __device__ __forceinline__ u4 x_chunk(const u4* xg, int kx, const XSlice& xs, XP
     return xg[static_cast<int64_t>(p.m) * kx + xs.c0 + p.c];
 }
 
+template <bool ONE_ROW>
 __device__ __forceinline__ void load_x_batch(u4 (&v)[kXB], const u4* xg, int kx, const XSlice& xs, int f0) {
 #pragma unroll
-    for (int j = 0; j < kXB; ++j) v[j] = x_chunk(xg, kx, xs, x_pos(xs, f0 + 64 * j));
+    for (int j = 0; j < kXB; ++j) v[j] = x_chunk(xg, kx, xs, x_pos<ONE_ROW>(xs, f0 + 64 * j));
 }
 
 // Flat chunk f into LDS. BIASED: as x' (pairs k = 8 j + 2, 3 and 8 j + 6, 7 divided by 16: exact, a
@@ -176,10 +180,10 @@ __device__ __forceinline__ void load_x_batch(u4 (&v)[kXB], const u4* xg, int kx,
 // for 8 j + 2, 3 and 8 j + 6, 7) dotted with x' give sum q x + 1024 sum x', so
 // sum (q - z) x = dot - 1024 A - z B. The four chunks of a 32-k slice are lanes 4 i .. 4 i + 3 of
 // one call (n16 and the lane offsets are multiples of 4); past the slice end all four or none.
-template <bool BIASED>
+template <bool BIASED, bool ONE_ROW>
 __device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, float2* corr, int kx, const XSlice& xs,
                                               u4 v, int f) {
-    const XPos p = x_pos(xs, f);
+    const XPos p = x_pos<ONE_ROW>(xs, f);
     const int col = xs.c0 + p.c;
     if constexpr (!BIASED) {
         smem[p.m * l.xs + col] = v;
@@ -188,16 +192,18 @@ __device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, floa
         const h2 hi = h2{static_cast<h1>(0.0625f), static_cast<h1>(0.0625f)};
         const h2 x0 = bitcast<h2>(v.x), x1 = bitcast<h2>(v.y), x2 = bitcast<h2>(v.z), x3 = bitcast<h2>(v.w);
         const h2 y0 = x0 * lo, y1 = x1 * hi, y2 = x2 * lo, y3 = x3 * hi;
-        float a = static_cast<float>(y0.x) + static_cast<float>(y0.y) + static_cast<float>(y1.x) +
-                  static_cast<float>(y1.y) + static_cast<float>(y2.x) + static_cast<float>(y2.y) +
-                  static_cast<float>(y3.x) + static_cast<float>(y3.y);
-        float b = static_cast<float>(x0.x) + static_cast<float>(x0.y) + static_cast<float>(x1.x) +
-                  static_cast<float>(x1.y) + static_cast<float>(x2.x) + static_cast<float>(x2.y) +
-                  static_cast<float>(x3.x) + static_cast<float>(x3.y);
-        a += __shfl_xor(a, 1);
-        b += __shfl_xor(b, 1);
-        a += __shfl_xor(a, 2);
-        b += __shfl_xor(b, 2);
+        float a = __builtin_amdgcn_fdot2(y0, lo, 0.0f, false);  // sums on v_dot2 (exact products by 1)
+        a = __builtin_amdgcn_fdot2(y1, lo, a, false);
+        a = __builtin_amdgcn_fdot2(y2, lo, a, false);
+        a = __builtin_amdgcn_fdot2(y3, lo, a, false);
+        float b = __builtin_amdgcn_fdot2(x0, lo, 0.0f, false);
+        b = __builtin_amdgcn_fdot2(x1, lo, b, false);
+        b = __builtin_amdgcn_fdot2(x2, lo, b, false);
+        b = __builtin_amdgcn_fdot2(x3, lo, b, false);
+        a += lane_xor1(a);
+        b += lane_xor1(b);
+        a += lane_xor2(a);
+        b += lane_xor2(b);
         smem[p.m * l.xs + col] =
             u4{bitcast<uint32_t>(y0), bitcast<uint32_t>(y1), bitcast<uint32_t>(y2), bitcast<uint32_t>(y3)};
         if ((col & 3) == 0 && f < xs.n) corr[p.m * (kx >> 2) + (col >> 2)] = float2{a, b};
@@ -206,16 +212,16 @@ __device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, floa
 
 // Stores the first batch (already loaded), then loads and stores the rest of the slice batch by
 // batch; ends with the wavefront's LDS writes ordered before its reads.
-template <bool BIASED>
+template <bool BIASED, bool ONE_ROW>
 __device__ __forceinline__ void stage_x(u4* smem, const DecodeLds& l, float2* corr, const u4* xg, int kx,
                                         const XSlice& xs, const u4 (&first)[kXB], int lane) {
 #pragma unroll
-    for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED>(smem, l, corr, kx, xs, first[j], lane + 64 * j);
+    for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, first[j], lane + 64 * j);
     for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {  // wavefront-uniform trip count
         u4 v[kXB];
-        load_x_batch(v, xg, kx, xs, f0);
+        load_x_batch<ONE_ROW>(v, xg, kx, xs, f0);
 #pragma unroll
-        for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED>(smem, l, corr, kx, xs, v[j], f0 + 64 * j);
+        for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, v[j], f0 + 64 * j);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -305,11 +311,11 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     WeightSet<U, NT> a, b;
     if (nch > 0) {
         u4 xfirst[kXB];
-        load_x_batch(xfirst, xg, kx, xsl, lane);
+        load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
         __builtin_amdgcn_sched_barrier(0);
         load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
         __builtin_amdgcn_sched_barrier(0);
-        stage_x<true>(smem, l, corr, xg, kx, xsl, xfirst, lane);
+        stage_x<true, M == 1>(smem, l, corr, xg, kx, xsl, xfirst, lane);
     }
 
     float acc[NT][M];
@@ -334,10 +340,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            float v = acc[t][m];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[t][m] = v;
+            acc[t][m] = sum_rows(acc[t][m]);
         }
     if (WK > 1) {
         float* red = reinterpret_cast<float*>(smem + l.red);  // [WK][NT * M][16]
@@ -453,11 +456,11 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         const XSlice xsl = x_slice(gb, ge, M);
         if (nch > 0) {
             u4 xfirst[kXB];
-            load_x_batch(xfirst, xg, kx, xsl, lane);
+            load_x_batch<false>(xfirst, xg, kx, xsl, lane);
             __builtin_amdgcn_sched_barrier(0);
             load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
             __builtin_amdgcn_sched_barrier(0);
-            stage_x<false>(smem, l, nullptr, xg, kx, xsl, xfirst, lane);
+            stage_x<false, false>(smem, l, nullptr, xg, kx, xsl, xfirst, lane);
         }
     } else {
         if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
@@ -504,10 +507,10 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
 #pragma unroll
             for (int bb = 0; bb < MT; ++bb) {
                 f4 up;
-                up.x = __shfl_xor(acc[t][bb].x, 32);
-                up.y = __shfl_xor(acc[t][bb].y, 32);
-                up.z = __shfl_xor(acc[t][bb].z, 32);
-                up.w = __shfl_xor(acc[t][bb].w, 32);
+                up.x = lane_xor32(acc[t][bb].x, lane);
+                up.y = lane_xor32(acc[t][bb].y, lane);
+                up.z = lane_xor32(acc[t][bb].z, lane);
+                up.w = lane_xor32(acc[t][bb].w, lane);
                 const int m = 16 * bb + r;
                 if (kb >= 2 || m >= M || tt >= tiles) continue;
                 const int f = 8 * tt + 4 * kb;  // features f .. f + 3 of the [M, N/2] output

@@ -269,10 +269,10 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
 #pragma unroll
             for (int b = 0; b < MT; ++b) {
                 f4 up;
-                up.x = __shfl_xor(acc[t][b].x, 32);
-                up.y = __shfl_xor(acc[t][b].y, 32);
-                up.z = __shfl_xor(acc[t][b].z, 32);
-                up.w = __shfl_xor(acc[t][b].w, 32);
+                up.x = lane_xor32(acc[t][b].x, lane);
+                up.y = lane_xor32(acc[t][b].y, lane);
+                up.z = lane_xor32(acc[t][b].z, lane);
+                up.w = lane_xor32(acc[t][b].w, lane);
                 const int m = m0 + 16 * b + r;
                 if (kb >= 2 || m >= M || tt >= tiles_n) continue;
                 const f4 g = acc[t][b];
