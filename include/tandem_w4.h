@@ -103,7 +103,11 @@ int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
  *   nt      16-row weight tiles per wavefront
  *   warps_n wavefronts along N (BN = 16 nt warps_n)
  *   warps_k wavefronts splitting each K step (1 or 2)
- *   stages  LDS ring depth (2: double buffering)
+ *   stages  2: x tiles through a double-buffered LDS ring, one barrier per K step;
+ *           0: small M: the unit's x rows over its whole K range resident in LDS (one barrier),
+ *           each wavefront streams its weight blocks with two groups in flight (every tile is
+ *           split: splits = 0 picks the fewest splits whose x slice fits, then enough units to
+ *           fill the GPU; a slice that cannot fit is refused with TW4_ECONFIG)
  *   splits  0: split only the last, partial wave of tiles along K; 1: no split; s > 1: every
  *           tile split s ways
  * ws (fp32, ws_floats) and locks (int32, n_locks, zero before the first call) are the split-K

@@ -53,6 +53,101 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
     return xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
 }
 
+// The end of a work unit, run by every thread of the workgroup. Wavefronts with `holder` set hold
+// the unit's fp32 tiles (rows 16 (wt0 + t) .., tokens m0 + 16 b ..) in acc. nsplit > 1: each stores
+// its partial to split slot su of ws; one agent-scope counter per split tile (st) tells the last
+// arriver, which adds the nsplit partials of the tile in split order (the result does not depend
+// on arrival order), returns the counter to zero for the next call and writes y. Partials and their
+// reads are agent-scope relaxed atomics (global_store / global_load sc1: coherent across the
+// XCDs' L2s without a cache-wide write-back or invalidate); each wavefront partial is stored
+// [fragment][component][lane], so every instruction moves 256 contiguous bytes. s_waitcnt vmcnt(0)
+// + barrier order the stores before the count. act = 1: SwiGLU epilogue (gate rows 4 kb + i and
+// up rows 8 + 4 kb + i sit in lanes l and l + 32).
+template <int MT, int NT, int WN>
+__device__ __forceinline__ void finish_unit(f4 (&acc)[NT][MT], bool holder, int wn, int lane, int tid, int nsplit,
+                                            int st, int su, float* __restrict__ ws, int* __restrict__ locks,
+                                            int& last_flag, h1* __restrict__ y, int M, int N, int m0, int wt0,
+                                            int tiles_n, int act) {
+    const int r = lane & 15, kb = lane >> 4;
+    if (nsplit > 1) {
+        constexpr int V = NT * MT * 4 * 64;  // floats per wavefront partial
+        if (holder) {
+            float* mine = ws + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        __hip_atomic_store(mine + ((t * MT + b) * 4 + c) * 64, acc[t][b][c], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = old == nsplit - 1;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        if (holder) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int v = 0; v < nsplit; ++v) {
+                const float* other = ws + ((static_cast<int64_t>(st) * nsplit + v) * WN + wn) * V + lane;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int b = 0; b < MT; ++b)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            acc[t][b][c] += __hip_atomic_load(other + ((t * MT + b) * 4 + c) * 64, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!holder) return;
+
+    if (act) {  // N % 16 == 0 (checked on the host)
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = wt0 + t;
+#pragma unroll
+            for (int b = 0; b < MT; ++b) {
+                f4 up;
+                up.x = lane_xor32(acc[t][b].x, lane);
+                up.y = lane_xor32(acc[t][b].y, lane);
+                up.z = lane_xor32(acc[t][b].z, lane);
+                up.w = lane_xor32(acc[t][b].w, lane);
+                const int m = m0 + 16 * b + r;
+                if (kb >= 2 || m >= M || tt >= tiles_n) continue;
+                const f4 g = acc[t][b];
+                const h4 o = h4{static_cast<h1>(silu(g.x) * up.x), static_cast<h1>(silu(g.y) * up.y),
+                                static_cast<h1>(silu(g.z) * up.z), static_cast<h1>(silu(g.w) * up.w)};
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + 8 * tt + 4 * kb) = o;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = 16 * (wt0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+        if (n >= N) continue;
+#pragma unroll
+        for (int b = 0; b < MT; ++b) {
+            const int m = m0 + 16 * b + r;
+            if (m >= M) continue;
+            const f4 a = acc[t][b];
+            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                h4{static_cast<h1>(a.x), static_cast<h1>(a.y), static_cast<h1>(a.z), static_cast<h1>(a.w)};
+        }
+    }
+}
+
 template <int MT, int NT, int WN, int WK, int ST>
 __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
     const h1* __restrict__ x, const u4* __restrict__ w, const h1* __restrict__ scales, const h1* __restrict__ zeros,
@@ -214,88 +309,204 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
         }
     }
 
-    if (nsplit > 1) {
-        // Partials and their reads are agent-scope relaxed atomics (global_store / global_load sc1:
-        // coherent across the XCDs' L2s without a cache-wide write-back or invalidate); each
-        // wavefront partial is stored [fragment][component][lane], so every instruction moves 256
-        // contiguous bytes. s_waitcnt vmcnt(0) + barrier order the stores before the count.
-        constexpr int V = NT * MT * 4 * 64;  // floats per wavefront partial
-        const int st = tile - dp;            // index among the split tiles
-        if (wk == 0) {
-            float* mine = ws + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+    finish_unit<MT, NT, WN>(acc, wk == 0, wn, lane, tid, nsplit, tile - dp, su, ws, locks, last_flag, y, M, N, m0, wt0,
+                            tiles_n, act);
+}
+
+// ------------------------------------------------------------------------ resident-x streaming
+// stages = 0: small-M variant. A work unit is one BM x BN output tile over one of `splits`
+// contiguous K ranges (every tile is split). The unit's x rows (only the M - m0 that exist) over
+// its whole K range are staged in LDS once, behind a single barrier; then every wavefront streams
+// its NT row tiles' weight blocks over its own contiguous sub-range of groups (WK wavefronts split
+// the unit's range) with U groups in flight ahead of the math in a second register set, like the
+// decode kernels, and no further barrier. Each lane loads either the scale (even kb) or the zero
+// (odd kb) of its row, one 2-byte load per tile and group; v_permlane16_swap hands every lane both.
+// LDS x image: row rho, group j, 16-byte chunk c at ((rho R + j) 16 + (c ^ (rho & 15))), R groups per
+// row, so the 16 rows of a B fragment read 16 different chunks.
+template <int U, int NT>
+struct StreamSet {
+    u4 w[U][NT];
+    uint32_t p[U][NT];  // scale (even kb) or zero (odd kb) of the lane's row
+};
+
+template <int MT, int NT, int WN, int WK, int U>
+struct StreamCfg {
+    static constexpr int BM = 16 * MT;
+    static constexpr int BN = 16 * NT * WN;
+    static constexpr int THREADS = WN * WK * 64;
+    static constexpr int RED = (WK - 1) * WN * NT * MT * 64;  // u4 (f4) of the K-wavefront reduction
+    static constexpr int XB = 8;                              // x chunks in flight per thread while staging
+};
+
+// LDS (u4) of a unit with `rows` x rows over `groups` groups.
+template <int MT, int NT, int WN, int WK, int U>
+__host__ __device__ __forceinline__ int stream_lds_u4(int rows, int groups) {
+    using C = StreamCfg<MT, NT, WN, WK, U>;
+    const int x = rows * groups * 16;
+    return x > C::RED ? x : C::RED;
+}
+
+template <int U, int NT>
+__device__ __forceinline__ void stream_load(StreamSet<U, NT>& ws, const u4* const (&wb)[NT], const uint16_t* const (&pb)[NT],
+                                            const int (&srows)[NT], int g0, int glast) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = min(g0 + u, glast);  // past the range: a valid block, given scale 0 below
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            ws.w[u][t] = load_stream(wb[t] + static_cast<int64_t>(g) * kBlockU4);
+            ws.p[u][t] = pb[t][static_cast<int64_t>(g) * srows[t]];
+        }
+    }
+}
+
+template <bool PF, int MT, int NT, int U>
+__device__ __forceinline__ void stream_chunk(const StreamSet<U, NT>& cur, StreamSet<U, NT>& nxt, const u4* const (&wb)[NT],
+                                             const uint16_t* const (&pb)[NT], const int (&srows)[NT],
+                                             const u4* const (&xrow)[MT], const int (&xsw)[MT], int g0, int ge, int glo,
+                                             f4 (&acc)[NT][MT], int kb, uint32_t magic) {
+    if constexpr (PF) stream_load<U, NT>(nxt, wb, pb, srows, g0 + U, ge - 1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math: the scheduler would sink it
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int graw = g0 + u;
+        const bool valid = graw < ge;
+        const int j = min(graw, ge - 1) - glo;  // group within the unit's range
+        GroupQ p[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const auto sz = __builtin_amdgcn_permlane16_swap(cur.p[u][t], cur.p[u][t], false, false);
+            p[t] = group_q(valid ? as_h1(sz[0]) : static_cast<h1>(0.0f), as_h1(sz[1]));
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            h8 xb[MT];
+#pragma unroll
+            for (int b = 0; b < MT; ++b) xb[b] = bitcast<h8>(xrow[b][j * 16 + ((4 * kb + s) ^ xsw[b])]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const h8 a = dequant_word(word_of(cur.w[u][t], s), p[t], magic);
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = mfma16x16x32(a, xb[b], acc[t][b]);
+            }
+        }
+    }
+}
+
+template <int MT, int NT, int WN, int WK, int U>
+__global__ void __launch_bounds__(WN * WK * 64) stream_kernel(
+    const h1* __restrict__ x, const u4* __restrict__ w, const h1* __restrict__ scales, const h1* __restrict__ zeros,
+    h1* __restrict__ y, float* __restrict__ ws, int* __restrict__ locks, int M, int N, int K, int mb, int nb,
+    int splits, int act) {
+    using C = StreamCfg<MT, NT, WN, WK, U>;
+    extern __shared__ u4 lds[];
+    __shared__ int last_flag;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave % WN, wk = wave / WN;
+    const int r = lane & 15, kb = lane >> 4;
+    const int G = K >> 7, tiles_n = (N + 15) >> 4;
+
+    const int unit = xcd_remap(blockIdx.x, gridDim.x);
+    const int tile = unit / splits, split = unit - tile * splits;
+    const int glo = static_cast<int>(static_cast<int64_t>(split) * G / splits);
+    const int ghi = static_cast<int>(static_cast<int64_t>(split + 1) * G / splits);
+    const int R = ghi - glo;
+    const int band = tile / (8 * nb), band_rows = min(mb - band * 8, 8), rin = tile - band * 8 * nb;
+    const int mblk = band * 8 + rin % band_rows, nblk = rin / band_rows;
+    const int m0 = mblk * C::BM;
+    const int rows = min(C::BM, M - m0);  // x rows that exist
+    const int wt0 = (nblk * WN + wn) * NT;
+
+    // stage x[m0 .. m0 + rows - 1][groups glo .. ghi - 1]: flat chunk f -> (row f / (16 R), chunk
+    // f % (16 R)); XB loads in flight per thread before their stores
+    {
+        const int r16 = 16 * R, total = rows * r16;
+        const uint32_t magic16 = 0xFFFFFFFFu / static_cast<uint32_t>(r16) + 1u;  // f / r16 = umulhi(f, magic16)
+        const u4* xg = reinterpret_cast<const u4*>(x);
+        const int kx = K >> 3;
+        for (int f0 = tid; f0 - tid < total; f0 += C::XB * C::THREADS) {  // workgroup-uniform trip count
+            u4 v[C::XB];
+            int dst[C::XB];
+#pragma unroll
+            for (int i = 0; i < C::XB; ++i) {
+                const int f = min(f0 + i * C::THREADS, total - 1);  // past the end: repeat the last chunk
+                const int rho = static_cast<int>(__umulhi(static_cast<uint32_t>(f), magic16));
+                const int c = f - rho * r16;
+                v[i] = xg[static_cast<int64_t>(m0 + rho) * kx + 16 * glo + c];
+                dst[i] = (rho * R + (c >> 4)) * 16 + ((c & 15) ^ (rho & 15));
+            }
+#pragma unroll
+            for (int i = 0; i < C::XB; ++i) lds[dst[i]] = v[i];
+        }
+    }
+
+    // this wavefront's groups and weight / parameter streams
+    const int gw = (R + WK - 1) / WK, gb = glo + min(wk * gw, R), ge = glo + min(wk * gw + gw, R);
+    const int nch = (ge - gb + U - 1) / U;
+    const u4* wb[NT];
+    const uint16_t* pb[NT];
+    int srows[NT];
+    const uint16_t* pbase = reinterpret_cast<const uint16_t*>((lane & 16) ? zeros : scales);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int tt = min(wt0 + t, tiles_n - 1);  // tiles past the end recompute the last one; not stored
+        wb[t] = w + static_cast<int64_t>(tt) * G * kBlockU4 + lane;
+        srows[t] = tile_rows(tt, N);
+        pb[t] = pbase + static_cast<int64_t>(16) * tt * G + min(r, srows[t] - 1);
+    }
+    const u4* xrow[MT];  // B column r of batch tile b = token row 16 b + r (rows past M read the last one)
+    int xsw[MT];         // that row's chunk swizzle
+#pragma unroll
+    for (int b = 0; b < MT; ++b) {
+        const int rho = min(16 * b + r, rows - 1);
+        xrow[b] = lds + rho * R * 16;
+        xsw[b] = rho & 15;
+    }
+    const uint32_t magic = magic_reg();
+
+    StreamSet<U, NT> a, b2;
+    if (nch > 0) stream_load<U, NT>(a, wb, pb, srows, gb, ge - 1);
+    __syncthreads();  // x staged
+
+    f4 acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int i = 0;
+    for (; i + 2 < nch; i += 2) {
+        stream_chunk<true, MT, NT, U>(a, b2, wb, pb, srows, xrow, xsw, gb + U * i, ge, glo, acc, kb, magic);
+        stream_chunk<true, MT, NT, U>(b2, a, wb, pb, srows, xrow, xsw, gb + U * (i + 1), ge, glo, acc, kb, magic);
+    }
+    if (i + 2 == nch) {
+        stream_chunk<true, MT, NT, U>(a, b2, wb, pb, srows, xrow, xsw, gb + U * i, ge, glo, acc, kb, magic);
+        stream_chunk<false, MT, NT, U>(b2, a, wb, pb, srows, xrow, xsw, gb + U * (i + 1), ge, glo, acc, kb, magic);
+    } else if (i + 1 == nch) {
+        stream_chunk<false, MT, NT, U>(a, b2, wb, pb, srows, xrow, xsw, gb + U * i, ge, glo, acc, kb, magic);
+    }
+
+    if constexpr (WK > 1) {  // fold wavefronts wk > 0 into wk = 0 (x is no longer read after the barrier)
+        __syncthreads();
+        f4* red = reinterpret_cast<f4*>(lds);
+        if (wk > 0) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int b = 0; b < MT; ++b)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        __hip_atomic_store(mine + ((t * MT + b) * 4 + c) * 64, acc[t][b][c], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) {
-            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_flag = old == splits - 1;
+                for (int bb = 0; bb < MT; ++bb) red[((((wk - 1) * WN + wn) * NT + t) * MT + bb) * 64 + lane] = acc[t][bb];
         }
         __syncthreads();
-        if (!last_flag) return;
         if (wk == 0) {
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            for (int v = 0; v < splits; ++v) {
-                const float* other = ws + ((static_cast<int64_t>(st) * splits + v) * WN + wn) * V + lane;
+            for (int v = 1; v < WK; ++v)
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int b = 0; b < MT; ++b)
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            acc[t][b][c] += __hip_atomic_load(other + ((t * MT + b) * 4 + c) * 64, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (wk != 0) return;
-
-    if (act) {  // N % 16 == 0 (checked on the host)
-        const int half_n = N >> 1;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int tt = wt0 + t;
-#pragma unroll
-            for (int b = 0; b < MT; ++b) {
-                f4 up;
-                up.x = lane_xor32(acc[t][b].x, lane);
-                up.y = lane_xor32(acc[t][b].y, lane);
-                up.z = lane_xor32(acc[t][b].z, lane);
-                up.w = lane_xor32(acc[t][b].w, lane);
-                const int m = m0 + 16 * b + r;
-                if (kb >= 2 || m >= M || tt >= tiles_n) continue;
-                const f4 g = acc[t][b];
-                const h4 o = h4{static_cast<h1>(silu(g.x) * up.x), static_cast<h1>(silu(g.y) * up.y),
-                                static_cast<h1>(silu(g.z) * up.z), static_cast<h1>(silu(g.w) * up.w)};
-                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + 8 * tt + 4 * kb) = o;
-            }
-        }
-        return;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int n = 16 * (wt0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
-        if (n >= N) continue;
-#pragma unroll
-        for (int b = 0; b < MT; ++b) {
-            const int m = m0 + 16 * b + r;
-            if (m >= M) continue;
-            const f4 a = acc[t][b];
-            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
-                h4{static_cast<h1>(a.x), static_cast<h1>(a.y), static_cast<h1>(a.z), static_cast<h1>(a.w)};
+                    for (int bb = 0; bb < MT; ++bb)
+                        acc[t][bb] += red[((((v - 1) * WN + wn) * NT + t) * MT + bb) * 64 + lane];
         }
     }
+    finish_unit<MT, NT, WN>(acc, wk == 0, wn, lane, tid, splits, tile, unit, ws, locks, last_flag, y, M, N, m0, wt0,
+                            tiles_n, act);
 }
 
 // Compiled GEMM configurations (MT, NT, WN, WK, ST).
@@ -303,6 +514,14 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
     X(1, 1, 4, 1, 2) X(1, 2, 4, 1, 2) X(2, 1, 4, 1, 2) X(2, 2, 4, 1, 2) X(2, 1, 4, 2, 2) X(2, 2, 4, 2, 2) \
     X(4, 1, 4, 1, 2) X(4, 2, 4, 1, 2) X(4, 2, 4, 2, 2) X(4, 4, 4, 1, 2) X(8, 1, 4, 1, 2) X(8, 2, 4, 1, 2) \
     X(8, 4, 4, 1, 2) X(8, 2, 2, 1, 2) X(4, 4, 2, 1, 2)
+
+// Compiled resident-x streaming configurations (MT, NT, WN, WK), stages = 0; kStreamU groups in flight.
+#define TW4_STREAM_CONFIGS(X)                                                                              \
+    X(1, 2, 4, 1) X(1, 4, 4, 1) X(1, 2, 4, 2) X(2, 2, 4, 1) X(2, 4, 4, 1) X(2, 2, 4, 2) X(4, 2, 4, 1) X(4, 4, 4, 1) \
+    X(4, 2, 4, 2) X(1, 2, 8, 1) X(2, 2, 8, 1)
+constexpr int kStreamU = 2;
+constexpr int kStreamAutoLds = 64 * 1024;  // splits = 0: the x slice of a unit stays within this
+constexpr int kMaxLdsBytes = 160 * 1024 - 256;  // dynamic LDS: gfx950 has 160 KB per workgroup, minus the static flag
 
 constexpr int kMaxDevices = 64;
 #define TW4_COUNT(MT, NT, WN, WK, ST) +1
@@ -371,6 +590,49 @@ int gemm_launch(int dev, int index, const h1* x, const u4* w, const h1* s, const
     return TW4_OK;
 }
 
+template <int MT, int NT, int WN, int WK>
+int stream_prepare() {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(stream_kernel<MT, NT, WN, WK, kStreamU>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "init: hipFuncSetAttribute (stream)");
+    return TW4_OK;
+}
+
+template <int MT, int NT, int WN, int WK>
+int stream_launch(int dev, const h1* x, const u4* w, const h1* s, const h1* z, h1* y, float* ws, int* locks,
+                  int64_t ws_floats, int64_t n_locks, int M, int N, int K, int splits, int act, hipStream_t stream) {
+    using C = StreamCfg<MT, NT, WN, WK, kStreamU>;
+    const int G = K >> 7;
+    const int mb = (M + C::BM - 1) / C::BM, tiles_n = (N + 15) >> 4;
+    const int nb = (tiles_n * 16 + C::BN - 1) / C::BN;
+    const int64_t tiles64 = static_cast<int64_t>(mb) * nb;
+    TW4_REQUIRE(tiles64 < (1LL << 26), TW4_EINVAL, "gemm: too many tiles (%lld)", static_cast<long long>(tiles64));
+    const int tiles = static_cast<int>(tiles64);
+    const int rows = M < C::BM ? M : C::BM;
+    int sp = splits;
+    if (sp == 0) {  // the fewest splits whose x slice fits the auto budget, then enough units for the GPU
+        sp = 1;
+        while (sp < G && 16LL * stream_lds_u4<MT, NT, WN, WK, kStreamU>(rows, (G + sp - 1) / sp) > kStreamAutoLds) ++sp;
+        while (sp < G && static_cast<int64_t>(tiles) * sp < 2LL * g_dev[dev].cus) ++sp;
+    }
+    TW4_REQUIRE(sp >= 1 && sp <= G, TW4_EINVAL, "gemm: splits %d for %d groups", sp, G);
+    const size_t lds = 16 * static_cast<size_t>(stream_lds_u4<MT, NT, WN, WK, kStreamU>(rows, (G + sp - 1) / sp));
+    TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLdsBytes), TW4_ECONFIG,
+                "gemm: the x slice of %d rows x %d groups does not fit in LDS (stages 0: use more splits)", rows,
+                (G + sp - 1) / sp);
+    if (sp > 1) {
+        TW4_REQUIRE(ws && locks, TW4_EINVAL, "gemm: split-K needs a workspace and counters");
+        TW4_REQUIRE(static_cast<int64_t>(tiles) * sp * C::BM * C::BN <= ws_floats && tiles <= n_locks, TW4_ESPACE,
+                    "gemm: split-K workspace too small for %d tiles x %d splits", tiles, sp);
+    }
+    const int64_t blocks = static_cast<int64_t>(tiles) * sp;
+    g_last_blocks = static_cast<int>(blocks), g_last_dp = 0, g_last_splits = sp;
+    stream_kernel<MT, NT, WN, WK, kStreamU><<<static_cast<unsigned>(blocks), C::THREADS, lds, stream>>>(
+        x, w, s, z, y, ws, locks, M, N, K, mb, nb, sp, act);
+    TW4_LAUNCH_CHECK("gemm: launch");
+    return TW4_OK;
+}
+
 int device_prepare(int dev) {
     if (dev < 0 || dev >= kMaxDevices) {
         tw4host::set_error("init: device %d out of range", dev);
@@ -387,6 +649,10 @@ int device_prepare(int dev) {
     ++index;
     TW4_GEMM_CONFIGS(TW4_PREP)
 #undef TW4_PREP
+#define TW4_SPREP(MT, NT, WN, WK) \
+    if (rc == TW4_OK) rc = stream_prepare<MT, NT, WN, WK>();
+    TW4_STREAM_CONFIGS(TW4_SPREP)
+#undef TW4_SPREP
     if (rc == TW4_OK) g_dev[dev].ready = 1;
     return rc;
 }
@@ -427,6 +693,14 @@ extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t
     auto zp = reinterpret_cast<const h1*>(zeros);
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
+    if (stages == 0) {
+#define TW4_STREAM_CASE(MT, NT, WN, WK)                                                                       \
+    if (mt == MT && nt == NT && warps_n == WN && warps_k == WK)                                                 \
+        return stream_launch<MT, NT, WN, WK>(dev, xp, wp, sp, zp, yp, ws, locks, ws_floats, n_locks, M, N, K, splits, \
+                                             act, st);
+        TW4_STREAM_CONFIGS(TW4_STREAM_CASE)
+#undef TW4_STREAM_CASE
+    }
     int index = 0;
 #define TW4_GEMM_CASE(MT, NT, WN, WK, ST)                                                                        \
     if (mt == MT && nt == NT && warps_n == WN && warps_k == WK && stages == ST)                                  \
@@ -460,5 +734,18 @@ extern "C" int tw4_gemm_configs(int* out, int max_configs) {
     ++n;
     TW4_GEMM_CONFIGS(TW4_LIST)
 #undef TW4_LIST
+#define TW4_SLIST(MT, NT, WN, WK) TW4_LIST(MT, NT, WN, WK, 0)
+#define TW4_LIST(MT, NT, WN, WK, ST)      \
+    if (out && n < max_configs) {         \
+        out[5 * n] = MT;                  \
+        out[5 * n + 1] = NT;              \
+        out[5 * n + 2] = WN;              \
+        out[5 * n + 3] = WK;              \
+        out[5 * n + 4] = ST;              \
+    }                                     \
+    ++n;
+    TW4_STREAM_CONFIGS(TW4_SLIST)
+#undef TW4_LIST
+#undef TW4_SLIST
     return n;
 }

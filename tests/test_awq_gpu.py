@@ -176,12 +176,15 @@ def test_mma_silu_mul(ext):
 
 
 def test_gemm_every_config(ext):
-    """M > 16 GEMM: every compiled config, partial token and row tiles, split-K of every tile or of
-    the last wave only; the counters are back at zero after each call (tests/test_awq.py:232-259)."""
+    """GEMM: every compiled config, partial token and row tiles, split-K of every tile or of the last
+    wave only (stages 0, the resident-x variant: the fewest splits that fit, chosen on the host); the
+    counters are back at zero after each call (tests/test_awq.py:232-259). A stages-0 config whose x
+    slice cannot fit in LDS for the requested splits is refused on the host, before any launch."""
     buf, locks = w4_hip.workspace(DEV)
+    ran = 0
     for k, n in SHAPES:
         c = Case(k, n, seed=7)
-        for m in (17, 40, 64, 130):
+        for m in (5, 17, 40, 64, 130):
             x = c.x(m, seed=400 + m)
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
@@ -189,10 +192,16 @@ def test_gemm_every_config(ext):
                 for splits in (0, 1, 3):
                     if splits > (k // 128 + cfg[3] - 1) // cfg[3]:
                         continue
-                    y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 0)
+                    try:
+                        y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 0)
+                    except RuntimeError as e:
+                        assert cfg[4] == 0 and "does not fit in LDS" in str(e), (cfg, splits, str(e))
+                        continue
+                    ran += 1
                     check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
     torch.cuda.synchronize()
     assert int(locks.abs().sum()) == 0
+    assert ran > len(GEMM_CONFIGS) * len(SHAPES)
 
 
 def test_gemm_silu_mul(ext):
@@ -208,7 +217,11 @@ def test_gemm_silu_mul(ext):
                 for splits in (0, 1, 2):
                     if splits > (k // 128 + cfg[3] - 1) // cfg[3]:
                         continue
-                    y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 1)
+                    try:
+                        y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, 1)
+                    except RuntimeError as e:
+                        assert cfg[4] == 0 and "does not fit in LDS" in str(e), (cfg, splits, str(e))
+                        continue
                     assert y.shape == (m, n // 2)
                     check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
     torch.cuda.synchronize()
@@ -220,9 +233,10 @@ def test_gemm_split_k_deterministic(ext):
     buf, locks = w4_hip.workspace(DEV)
     c = Case(4096, 1024, seed=9)
     xg = gpu(c.x(33, seed=9))
-    first = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, 2, 1, 4, 1, 2, 8, 0)
-    for _ in range(5):
-        assert torch.equal(ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, 2, 1, 4, 1, 2, 8, 0), first)
+    for cfg in ((2, 1, 4, 1, 2, 8), (2, 2, 4, 1, 0, 8)):  # LDS ring; resident x
+        first = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, 0)
+        for _ in range(5):
+            assert torch.equal(ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, 0), first)
 
 
 def test_gemm_split_k_graph_replay(ext):
