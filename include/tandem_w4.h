@@ -121,6 +121,17 @@ int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
              void* stream);
 
+/* Dense fp16 GEMV for small batches: y [M, N] = x [M, K] @ w [N, K]^T (w row-major, nn.Linear
+ * layout), 1 <= M <= 8, K in {512, 1024, 2048, 4096}, fp32 accumulation; x and w 16-byte aligned.
+ * Config: rows_inflight rows per wavefront in flight (plus the next block prefetched), rows_per_wave
+ * contiguous rows per wavefront. For the fp16 lm_head of a W4A16 model.
+ * Replaces gemv / _gemv_kernel (python/tandem/layers/triton_gemv.py:26-61, 180-218). */
+int tw4_gemv_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,
+                 int rows_inflight, int rows_per_wave, void* stream);
+
+/* Compiled (rows_inflight, rows_per_wave) configurations of tw4_gemv_f16; returns how many. */
+int tw4_gemv_f16_configs(int* out, int max_configs);
+
 /* Compiled configurations, for sweeps and tests (the reference lists them in its host code,
  * python/tandem/csrc/w4_gemv.cu:596-597, 641-645, 676-679). Each writes up to max_configs
  * tuples into out and returns how many exist: tw4_decode_configs (warps_k, unroll, ntile) for

@@ -48,6 +48,8 @@ _SIGNATURES = {
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
+    "tw4_gemv_f16": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "tw4_gemv_f16_configs": ([ctypes.POINTER(_I), _I], _I),
 }
 
 
@@ -80,6 +82,11 @@ def decode_configs() -> tuple[tuple[int, int, int], ...]:
 def gemm_configs() -> tuple[tuple[int, int, int, int, int], ...]:
     """The compiled (mt, nt, warps_n, warps_k, stages) configurations of w4_gemm."""
     return _configs("tw4_gemm_configs", 5)
+
+
+def gemv_f16_configs() -> tuple[tuple[int, int], ...]:
+    """The compiled (rows in flight, rows per wavefront) configurations of tw4_gemv_f16."""
+    return _configs("tw4_gemv_f16_configs", 2)
 
 
 def check(status: int) -> None:

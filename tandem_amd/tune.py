@@ -3,6 +3,7 @@ benchmarks/bench_w4.py and bench_w4_gemm.py, which produced its per-GPU tables.
 
     python -m tandem_amd.tune --model qwen3-8b --ms 1,4,8,16 --kinds gemv,mma [--out sweep.jsonl]
     python -m tandem_amd.tune --model qwen3-8b --ms 24,32,64,256 --kinds gemm
+    python -m tandem_amd.tune --model qwen3-8b --projs lm_head --ms 1,2,4,8 --kinds dense16,torch16
 
 For each projection shape and M, every compiled configuration of each kernel is timed the way
 the reference timed them (benchmarks/bench_gemv.py:35-56): one HIP graph replays `rounds` passes
@@ -23,10 +24,13 @@ import torch
 from tandem_amd.layers import w4_hip
 
 MODELS = {
-    "qwen3-8b": {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)},
-    "qwen3-1.7b": {"qkv": (2048, 4096), "o": (2048, 2048), "gate_up": (2048, 12288), "down": (6144, 2048)},
-    "qwen3-0.6b": {"qkv": (1024, 4096)},
+    "qwen3-8b": {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096),
+                 "lm_head": (4096, 151936)},
+    "qwen3-1.7b": {"qkv": (2048, 4096), "o": (2048, 2048), "gate_up": (2048, 12288), "down": (6144, 2048),
+                   "lm_head": (2048, 151936)},
+    "qwen3-0.6b": {"qkv": (1024, 4096), "lm_head": (1024, 151936)},
 }
+DENSE = ("lm_head",)  # fp16 projections (kinds dense16 / torch16); the others are W4A16
 
 
 def call_bytes(m: int, k: int, n: int) -> int:
@@ -65,6 +69,23 @@ def time_us(calls, stream, rounds: int = 10, reps: int = 5) -> float:
     return t0.elapsed_time(t1) * 1e3 / (reps * rounds * len(calls))
 
 
+def emit(a, out, proj: str, k: int, n: int, m: int, act: int, copies: int, res: dict, b: int) -> None:
+    """One JSON record: the best config, us/call, GB/s of the algorithmic bytes b, every config."""
+    if not res:
+        return
+    best = min(res, key=res.get)
+    rec = {"model": a.model, "proj": proj, "k": k, "n": n, "m": m, "act": act, "copies": copies,
+           "best": list(best), "us": round(res[best], 3), "GBps": round(b / res[best] / 1e3, 1),
+           "pct_hbm_peak": round(b / res[best] / 1e3 / 80, 2),
+           "TFLOPs": round(2 * m * k * n / res[best] / 1e6, 2),
+           "best_per_kind": {kd: min((v, list(c)) for c, v in res.items() if c[0] == kd)
+                             for kd in {c[0] for c in res}},
+           "all": {"/".join(map(str, c)): round(v, 2) for c, v in sorted(res.items(), key=lambda kv: kv[1])}}
+    print(json.dumps(rec), flush=True)
+    if out:
+        out.write(json.dumps(rec) + "\n")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--model", default="qwen3-8b", choices=sorted(MODELS))
@@ -90,6 +111,28 @@ def main(argv=None) -> int:
         if a.act and proj != "gate_up":
             continue
         act = int(a.act)
+        if (proj in DENSE) != any(kd in kinds for kd in ("dense16", "torch16")):
+            continue
+        if proj in DENSE:  # fp16 weights [N, K]: the kernel of layers/gemv16.py against F.linear
+            from tandem_amd.layers import gemv16
+
+            wbytes = 2 * n * k
+            copies = max(1, math.ceil(a.footprint_mb * 1e6 / wbytes))
+            wd = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).half() for _ in range(copies)]
+            for m in (int(v) for v in a.ms.split(",")):
+                x = torch.randn(m, k, device=dev, dtype=torch.float16)
+                res = {}
+                if "dense16" in kinds:
+                    for cfg in w4_hip.gemv_f16_configs():
+                        res[("dense16", *cfg)] = time_us([lambda w=w, c=cfg: gemv16.gemv(x, w, *c) for w in wd],
+                                                         stream, rounds=3)
+                if "torch16" in kinds:
+                    res[("torch16",)] = time_us([lambda w=w: torch.nn.functional.linear(x, w) for w in wd], stream,
+                                                rounds=3)
+                emit(a, out, proj, k, n, m, 0, copies, res, wbytes + 2 * m * k + 2 * m * n)
+            del wd
+            torch.cuda.empty_cache()
+            continue
         wbytes = call_bytes(0, k, n)
         copies = max(2, math.ceil(a.footprint_mb * 1e6 / wbytes))
         ws = [random_weights(k, n, dev, gen) for _ in range(copies)]
@@ -130,20 +173,7 @@ def main(argv=None) -> int:
                     return awq.silu_and_mul(y) if act else y
 
                 res[("dense",)] = time_us([lambda w=w: dense(w) for w in ws[:8]], stream, rounds=3)
-            if not res:
-                continue
-            best = min(res, key=res.get)
-            b = call_bytes(m, k, n)
-            rec = {"model": a.model, "proj": proj, "k": k, "n": n, "m": m, "act": act, "copies": copies,
-                   "best": list(best), "us": round(res[best], 3), "GBps": round(b / res[best] / 1e3, 1),
-                   "pct_hbm_peak": round(b / res[best] / 1e3 / 80, 2),
-                   "TFLOPs": round(2 * m * k * n / res[best] / 1e6, 2),
-                   "best_per_kind": {kd: min((v, list(c)) for c, v in res.items() if c[0] == kd)
-                                     for kd in {c[0] for c in res}},
-                   "all": {"/".join(map(str, c)): round(v, 2) for c, v in sorted(res.items(), key=lambda kv: kv[1])}}
-            print(json.dumps(rec), flush=True)
-            if out:
-                out.write(json.dumps(rec) + "\n")
+            emit(a, out, proj, k, n, m, act, copies, res, call_bytes(m, k, n))
         del ws
         torch.cuda.empty_cache()
     if out:
