@@ -18,6 +18,9 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
                 numpy) on a bounded sample of the same workload, on this host's cores
   detail        per projection and M in {1, 8, 32}: us/call, GB/s, % of peak, TFLOP/s, the kernel
                 that ran, and at M = 32 the dequantize + torch.matmul comparator
+  full_stack    the whole decode step of the linears plus the fp16 lm_head (4096 x 151936, through
+                layers/gemv16.py's table: the HIP fp16 GEMV where it has an entry, else F.linear),
+                M in {1, 8, 32}: us per step and GB/s
 """
 
 from __future__ import annotations
@@ -34,6 +37,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, AMD public spec
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, AMD public spec
 QWEN3_8B = (("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576), ("down", 12288, 4096))
+LM_HEAD = (4096, 151936)  # Qwen3-8B vocabulary x hidden, fp16
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_m1.json")
 
 
@@ -234,6 +238,34 @@ def main() -> int:
                 detail[f"{proj}_m{mm}"] = rec
             torch.cuda.synchronize()
 
+    full = {}
+    if not a.no_detail:
+        from tandem_amd.layers import gemv16
+
+        hk, hn = LM_HEAD
+        head = (torch.randn(hn, hk, device=dev, dtype=torch.float16) * 0.02)
+        table = gemv16.table_for(dev, torch.nn.Module())
+        for mm in (1, 8, 32):
+            xd = {4096: torch.randn(mm, 4096, device=dev, dtype=torch.float16),
+                  12288: torch.randn(mm, 12288, device=dev, dtype=torch.float16)}
+
+            def full_step():
+                for layer in layers:
+                    for proj, k, n in QWEN3_8B:
+                        layer[proj](xd[k])
+                gemv16.linear(xd[4096], head, table)
+
+            g = graph_of(torch, full_step, stream)
+            us = time_graph(torch, g, stream, reps=10) * 1e6
+            del g
+            b = a.layers * sum(call_bytes(mm, k, n) for _, k, n in QWEN3_8B) + 2 * hn * hk + 2 * mm * (hk + hn)
+            full[f"m{mm}"] = {"us_per_step": round(us, 1), "GBps": round(b / us / 1e3, 1),
+                              "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1), "step_bytes": b,
+                              "lm_head": "gemv16" if table.get((hn, hk, gemv16.m_bucket(mm))) and mm <= 8
+                              else "F.linear"}
+        del head
+        torch.cuda.synchronize()
+
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds, m)
     line = {
         "metric": "W4A16 us/call + achieved HBM GB/s (% peak), Qwen3-8B shapes, M=1/8/32",
@@ -246,7 +278,7 @@ def main() -> int:
                    "step_bytes": step_bytes, "step_flops": step_flops},
         "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
         "us_per_layer": round(step_s / a.layers * 1e6, 2),
-        "roofline": roofline, "cpu_baseline": cpu, "detail": detail,
+        "roofline": roofline, "cpu_baseline": cpu, "detail": detail, "full_stack": full,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(line), flush=True)
