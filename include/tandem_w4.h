@@ -87,6 +87,15 @@ int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              const uint16_t* zeros, uint16_t* y, int M, int N, int K,
              int warps_k, int unroll, int ntile, void* stream);
 
+/* tw4_gemv with tw4_mma's act argument: act = 1 writes y = silu(gate) * up, [M, N/2], rows in
+ * interleave_gate_up order (N % 16 == 0); act = 0 is tw4_gemv. The reference's GEMV has no
+ * SwiGLU epilogue (python/tandem/csrc/w4_gemv.cu:96-153), so its SwiGLU gate_up takes w4_mma at
+ * every decode M (python/tandem/layers/awq.py:253-270); this entry lets a W4Linear table send
+ * M <= 4 SwiGLU gate_up to the GEMV. */
+int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+                 const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+                 int warps_k, int unroll, int ntile, int act, void* stream);
+
 /* Decode on the matrix cores (v_mfma_f32_16x16x32_f16, weights as the A operand, the batch on
  * the 16-column side, ceil(M / 16) column tiles), 1 <= M <= 64; unroll * ceil(M / 16) <= 4.
  * act = 1: y = silu(gate) * up, [M, N/2], rows in interleave_gate_up order (N % 16 == 0);

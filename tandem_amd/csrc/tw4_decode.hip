@@ -29,9 +29,10 @@
 //         M - 1: they only feed D columns that are never stored. D holds output rows 4 kb + i
 //         (i = 0..3) of batch column r in lane (kb, r). x comes from LDS when M (K + 8) 2 bytes
 //         fit in 80 KB, else straight from global memory (issued before the prefetch).
-//   act = 1 (mma): rows are in interleave_gate_up order, so the gate rows 4 kb + i (kb = 0, 1)
-//         and up rows 8 + 4 kb + i of a feature sit in lanes l and l + 32; one cross-lane
-//         exchange pairs them and the lane writes silu(gate) * up.
+//   act = 1: rows are in interleave_gate_up order (gate rows 0..7 of a tile, then its up rows).
+//         mma: the gate rows 4 kb + i (kb = 0, 1) and up rows 8 + 4 kb + i of a feature sit in
+//         lanes l and l + 32; gemv: in lanes i and i + 8. One cross-lane exchange pairs them and
+//         the lane writes silu(gate) * up.
 #include "tw4_common.h"
 
 namespace tw4 {
@@ -290,7 +291,7 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
 template <int M, int WK, int U, int NT>
 __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                       const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                      h1* __restrict__ y, int N, int K) {
+                                                      h1* __restrict__ y, int N, int K, int act) {
     extern __shared__ u4 smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
@@ -358,6 +359,21 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[t][m] += red[(v * NT * M + t * M + m) * 16 + r];
+    }
+    if (act) {  // N % 16 == 0 (checked on the host): gate row i of the tile in lane i, up row 8 + i in lane i + 8
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = tile0 + t;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float up = __int_as_float(
+                    __builtin_amdgcn_update_dpp(0, __float_as_int(acc[t][m]), 0x128, 0xF, 0xF, false));  // row_ror:8
+                if (kb == 0 && r < 8 && tt < tiles)
+                    y[static_cast<int64_t>(m) * half_n + 8 * tt + r] = static_cast<h1>(silu(acc[t][m]) * up);
+            }
+        }
+        return;
     }
     if (kb != 0) return;
 #pragma unroll
@@ -587,14 +603,14 @@ int ensure_prepared() {
 
 template <int M>
 int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
-                  hipStream_t st) {
+                  int act, hipStream_t st) {
     const int tiles = (N + 15) >> 4;
 #define TW4_GEMV_CASE(WK, U, T)                                                                              \
     if (wk == WK && un == U && nt == T) {                                                                    \
         const size_t lds = 16 * static_cast<size_t>(decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, T)).total); \
         TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
                     "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);          \
-        gemv_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K);            \
+        gemv_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act);       \
         TW4_LAUNCH_CHECK("gemv: launch");                                                                    \
         return TW4_OK;                                                                                       \
     }
@@ -621,12 +637,15 @@ using namespace tw4;
 
 int tw4_decode_prepare_device(int dev) { return decode_prepare(dev); }
 
-extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
-                        uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, void* stream) {
+extern "C" int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                            uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, int act,
+                            void* stream) {
     int rc = check_operands("gemv", x, packed, scales, zeros, y, M, N, K);
     if (rc) return rc;
     TW4_REQUIRE(M >= 1 && M <= 4, TW4_EINVAL, "gemv: 1 <= M <= 4 (M = %d; larger M: mma)", M);
     TW4_REQUIRE(K <= 65536, TW4_EINVAL, "gemv: K <= 65536 (K = %d; larger K: mma)", K);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "gemv: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
     rc = ensure_prepared();
     if (rc) return rc;
     auto xp = reinterpret_cast<const h1*>(x);
@@ -636,11 +655,16 @@ extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
     switch (M) {
-        case 1: return gemv_dispatch<1>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, st);
-        case 2: return gemv_dispatch<2>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, st);
-        case 3: return gemv_dispatch<3>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, st);
-        default: return gemv_dispatch<4>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, st);
+        case 1: return gemv_dispatch<1>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        case 2: return gemv_dispatch<2>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        case 3: return gemv_dispatch<3>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        default: return gemv_dispatch<4>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
     }
+}
+
+extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                        uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, void* stream) {
+    return tw4_gemv_act(x, packed, scales, zeros, y, M, N, K, warps_k, unroll, ntile, 0, stream);
 }
 
 extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,

@@ -108,8 +108,8 @@ def repack_awq(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor
 
 def interleave_gate_up(t: torch.Tensor) -> torch.Tensor:
     """Rows [gate (I); up (I)] -> tiles of 16 rows [gate 8i .. 8i+7, up 8i .. 8i+7], the order in
-    which the matrix-core kernels' SwiGLU epilogue finds gate and up of a feature in lanes l and
-    l + 32 (python/tandem/layers/awq.py:71-75). For row-major tensors (scales, zeros, dense
+    which the kernels' SwiGLU epilogues find gate and up of a feature in paired lanes
+    (python/tandem/layers/awq.py:71-75). For row-major tensors (scales, zeros, dense
     weights, before tile_major_params); the tile-layout `packed` is interleaved by
     repack_awq(..., interleave=True)."""
     n = t.shape[0]
@@ -137,7 +137,8 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 
 # Decode kernel per GPU and (N, K, M) / (N, K, M, "silu") for M <= 16, the fastest of
 # `python -m tandem_amd.tune` sweeps on the GPU:
-#   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4, no SwiGLU epilogue
+#   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4 (with the SwiGLU epilogue too: the
+#                                      reference's SwiGLU gate_up always takes "mma")
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
 #   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
@@ -216,8 +217,8 @@ class W4Linear(nn.Module):
     (python/tandem/layers/awq.py:206-286).
 
     ``enable_silu_mul`` (gate_up of a SwiGLU MLP, before ``finalize``): the layer returns
-    silu(gate) * up, [M, out_features / 2], instead of [gate | up]; the matrix-core kernels apply
-    it in their epilogue (rows reordered as interleave_gate_up)."""
+    silu(gate) * up, [M, out_features / 2], instead of [gate | up]; the kernels apply it in their
+    epilogue (rows reordered as interleave_gate_up)."""
 
     def __init__(self, in_features: int, out_features: int, group: int) -> None:
         super().__init__()
@@ -281,9 +282,9 @@ class W4Linear(nn.Module):
                 kind, *cfg = entry
                 if kind == "gemm":
                     return self._gemm(ext, x, cfg)
-                if kind == "gemv" and m <= 4 and not self.silu_mul:
-                    return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg)
-                if kind != "mma":  # gemv past M = 4, or with the SwiGLU epilogue
+                if kind == "gemv" and m <= 4:  # with the SwiGLU epilogue too (tw4_gemv_act)
+                    return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
+                if kind != "mma":  # gemv past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
         elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul

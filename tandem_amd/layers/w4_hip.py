@@ -43,6 +43,7 @@ _SIGNATURES = {
     "tw4_repack_awq": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "tw4_dequant": ([_P, _P, _P, _P, _I, _I, _I, _P], _I),
     "tw4_gemv": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tw4_gemv_act": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
@@ -151,14 +152,17 @@ class W4Extension:
     def __init__(self) -> None:
         self.lib = library()
 
-    def w4_gemv(self, x, w, s, z, warps_k: int, unroll: int, ntile: int) -> torch.Tensor:
+    def w4_gemv(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int = 0) -> torch.Tensor:
+        """act = 1 (not in the reference's w4_gemv): the SwiGLU epilogue of w4_mma."""
         m, n, k = check_operands("w4_gemv", x, w, s, z)
         if not 1 <= m <= 4:
             raise RuntimeError("w4_gemv: M <= 4 (larger M: w4_mma)")
-        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+        if act not in (0, 1) or (act and n % 16):
+            raise RuntimeError("w4_gemv: act 0, or 1 (SwiGLU) with N % 16 == 0")
+        y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
         with torch.cuda.device(x.device):
-            check(self.lib.tw4_gemv(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
-                                    int(warps_k), int(unroll), int(ntile), _stream(x)))
+            check(self.lib.tw4_gemv_act(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
+                                        int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
         return y
 
     def w4_mma(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int) -> torch.Tensor:

@@ -139,10 +139,10 @@ def main(argv=None) -> int:
         for m in (int(v) for v in a.ms.split(",")):
             x = torch.randn(m, k, device=dev, dtype=torch.float16)
             res = {}
-            if "gemv" in kinds and m <= 4 and not act:
+            if "gemv" in kinds and m <= 4:
                 for cfg in w4_hip.decode_configs():
                     try:
-                        us = time_us([lambda w=w, c=cfg: ext.w4_gemv(x, *w, *c) for w in ws], stream)
+                        us = time_us([lambda w=w, c=cfg: ext.w4_gemv(x, *w, *c, act) for w in ws], stream)
                     except RuntimeError:
                         continue
                     res[("gemv", *cfg)] = us

@@ -113,6 +113,21 @@ def test_gemv_every_config(ext):
                 check_close(ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg))
 
 
+def test_gemv_silu_mul(ext):
+    """The GEMV with the SwiGLU epilogue (tw4_gemv_act, act = 1; the reference's GEMV has none) on
+    interleaved rows, M = 1..4, every compiled config, at the GEMV's tolerance."""
+    for k, n in ((128, 32), (1024, 512), (4096, 1024)):
+        c = Case(k, n, seed=16, interleave=True)
+        for m in range(1, 5):
+            x = c.x(m, seed=800 + m)
+            ref = o.swiglu_reference(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                y = ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg, 1)
+                assert y.shape == (m, n // 2)
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
+
+
 def test_mma_every_config(ext):
     """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229)."""
     for k, n in SHAPES:

@@ -75,6 +75,8 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 5, 64, 128, 4, 2, 1, None), "M <= 4"),
         (lambda: lib.tw4_gemv(_fake(4100), _fake(), _fake(), _fake(), _fake(), 1, 64, 128, 4, 2, 1, None), "aligned"),
         (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 64, 65536 + 128, 1, 4, 1, None), "K <= 65536"),
+        (lambda: lib.tw4_gemv_act(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 24, 128, 4, 2, 1, 1, None),
+         "SwiGLU"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 65, 64, 128, 4, 2, 1, 0, None), "M <= 64"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
@@ -206,9 +208,9 @@ def test_tables_are_well_formed():
             assert 1 <= m <= 16 and k % 128 == 0 and n % 8 == 0
             if cfg[0] == "gemm":  # a compiled GEMM config and a split mode
                 assert len(cfg) == 7 and tuple(cfg[1:6]) in gemm and 0 <= cfg[6] <= 16
-            else:  # a compiled decode config; gemv only where it runs (M <= 4, no epilogue)
+            else:  # a compiled decode config; gemv only where it runs (M <= 4)
                 assert cfg[0] in ("gemv", "mma") and tuple(cfg[1:]) in decode
-                assert cfg[0] == "mma" or (m <= 4 and len(key) == 3)
+                assert cfg[0] == "mma" or m <= 4
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
         m_maxes = [m for m, _ in ladder]
         assert m_maxes == sorted(m_maxes)
