@@ -141,6 +141,21 @@ int tw4_gemv_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N
 /* Compiled (rows_inflight, rows_per_wave) configurations of tw4_gemv_f16; returns how many. */
 int tw4_gemv_f16_configs(int* out, int max_configs);
 
+/* RMSNorm of the decoder layer around the projections, fp16 rows [M, K], fp32 math, K % 512 == 0,
+ * K <= 8192, rows 16-byte aligned. y = fp16(x * rsqrt(mean(x^2) + eps) * weight).
+ * Replaces ops.rms_norm of the GPU path (python/tandem/layers/ops.py:107-109, FlashInfer's
+ * rmsnorm: fp32 math, one rounding). */
+int tw4_rms_norm(const uint16_t* x, const uint16_t* weight, uint16_t* y, int M, int K, float eps,
+                 void* stream);
+
+/* Residual add + RMSNorm, in place: s = x + residual in fp32; residual <- fp16(s);
+ * x <- fp16(s * rsqrt(mean(s^2) + eps) * weight). Same limits as tw4_rms_norm.
+ * Replaces ops.fused_add_rms_norm (python/tandem/layers/ops.py:111-120; the Triton kernel of
+ * python/tandem/layers/triton_ops.py:101-124 and FlashInfer's fused_add_rmsnorm). The sum of
+ * squares is taken in the same fixed order as the decode kernels' fused norm prologue. */
+int tw4_add_rms_norm(uint16_t* x, uint16_t* residual, const uint16_t* weight, int M, int K,
+                     float eps, void* stream);
+
 /* Compiled configurations, for sweeps and tests (the reference lists them in its host code,
  * python/tandem/csrc/w4_gemv.cu:596-597, 641-645, 676-679). Each writes up to max_configs
  * tuples into out and returns how many exist: tw4_decode_configs (warps_k, unroll, ntile) for

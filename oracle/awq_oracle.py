@@ -21,11 +21,16 @@ relative to its repository root):
                                weights
     random_awq                 the reference tests' input recipe   tests/test_awq.py:32-38
                                (numpy's generator, not CUDA's)
+    rms_norm                   fp16(x rstd w), fp32 semantics      python/tandem/layers/ops.py:107-109
+    add_rms_norm               s = x + r (fp32); r' = fp16(s);     python/tandem/layers/triton_ops.py:101-124,
+                               y = fp16(s rstd w)                  python/tandem/layers/ops.py:111-120
 
 What pins each function (tests/test_oracle.py): known-answer words and the test packer's inverse
 for the nibble order; brute force over every (q, z) pair against exact rational arithmetic for the
-dequantization; closed forms for the interleave; explicit loops for the matmul; and planted
-mistakes (swapped orders, double rounding, transposed operands) that those checks must reject.
+dequantization; closed forms for the interleave; explicit loops for the matmul; closed forms
+(constant rows, eps-dominated rows) and explicit loops for the norms; and planted mistakes
+(swapped orders, double rounding, transposed operands, a dropped eps or residual) that those checks
+must reject.
 No function of this module is "parity unpinned".
 """
 
@@ -143,3 +148,23 @@ def dequant_then_linear(x: np.ndarray, qweight: np.ndarray, qzeros: np.ndarray, 
     w = dequant(qweight, qzeros, scales, group)
     y = np.asarray(x, dtype=matmul_dtype) @ w.astype(matmul_dtype).T
     return y.astype(out_dtype)
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """y = fp16(x * rsqrt(mean(x^2) + eps) * w) over the last axis, the reference GPU path's
+    rmsnorm (python/tandem/layers/ops.py:107-109: fp32 math, one rounding); the mean and the
+    products in float64 here."""
+    x64 = np.asarray(x, dtype=np.float16).astype(np.float64)
+    rstd = 1.0 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + eps)
+    return (x64 * rstd * np.asarray(w, dtype=np.float16).astype(np.float64)).astype(np.float16)
+
+
+def add_rms_norm(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float) -> tuple[np.ndarray, np.ndarray]:
+    """(y, r') of the residual add + RMSNorm (python/tandem/layers/triton_ops.py:101-124):
+    s = x + r in float32, r' = fp16(s), y = fp16(s * rsqrt(mean(s^2) + eps) * w) from the
+    unrounded s."""
+    s = np.asarray(x, dtype=np.float16).astype(np.float32) + np.asarray(r, dtype=np.float16).astype(np.float32)
+    s64 = s.astype(np.float64)
+    rstd = 1.0 / np.sqrt(np.mean(s64 * s64, axis=-1, keepdims=True) + eps)
+    y = (s64 * rstd * np.asarray(w, dtype=np.float16).astype(np.float64)).astype(np.float16)
+    return y, s.astype(np.float16)

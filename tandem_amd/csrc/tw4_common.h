@@ -121,6 +121,53 @@ __device__ __forceinline__ float sum_rows(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Sum of the 16 lanes of each row (lanes 16 i .. 16 i + 15), the same bits in all 16 lanes: every
+// step adds the values of a lane pair that exchange with each other (l ^ 1, l ^ 2, then DPP
+// row_half_mirror and row_mirror), and floating-point addition is commutative.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // row mirror
+    return v;
+}
+
+// Sum over the 64 lanes, the same bits in every lane: (R0 + R1) + (R2 + R3) of the row sums.
+__device__ __forceinline__ float wave_total(float v) { return sum_rows(row16_sum(v)); }
+
+// Sum of squares of 8 fp32 values in a fixed order (all fma, so no contraction choice is left to
+// the compiler).
+__device__ __forceinline__ float sumsq8(const float (&s)[8]) {
+    float q = __builtin_fmaf(s[0], s[0], 0.0f);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) q = __builtin_fmaf(s[i], s[i], q);
+    return q;
+}
+
+// 8 halves of a 16-byte chunk as fp32, and 8 fp32 values rounded (RNE) into a chunk.
+__device__ __forceinline__ void chunk_to_f32(const u4& v, float (&f)[8]) {
+    const h2 a = bitcast<h2>(v.x), b = bitcast<h2>(v.y), c = bitcast<h2>(v.z), d = bitcast<h2>(v.w);
+    f[0] = a.x, f[1] = a.y, f[2] = b.x, f[3] = b.y, f[4] = c.x, f[5] = c.y, f[6] = d.x, f[7] = d.y;
+}
+__device__ __forceinline__ u4 f32_to_chunk(const float (&f)[8]) {
+    return u4{bitcast<uint32_t>(h2{static_cast<h1>(f[0]), static_cast<h1>(f[1])}),
+              bitcast<uint32_t>(h2{static_cast<h1>(f[2]), static_cast<h1>(f[3])}),
+              bitcast<uint32_t>(h2{static_cast<h1>(f[4]), static_cast<h1>(f[5])}),
+              bitcast<uint32_t>(h2{static_cast<h1>(f[6]), static_cast<h1>(f[7])})};
+}
+
+// RMS normalisation with its sum of squares in one fixed order, shared by the norm kernels and the
+// decode kernels' fused norm prologue, so both produce the same bits. For a row of K halves
+// (K % 128 == 0): chunk c = values 8 c .. 8 c + 7 gives q_c = sumsq8; quant group g (chunks
+// 16 g .. 16 g + 15, held by lanes 16 i .. 16 i + 15 of one row of a wavefront) gives
+// S_g = row16_sum(q); lane l of one wavefront adds S_l, S_(l+64), ... in increasing order and
+// wave_total adds the lanes. rstd = rsqrt(total / K + eps).
+__device__ __forceinline__ float norm_rstd(const float* gsum, int G, int K, float eps, int lane) {
+    float t = 0.0f;
+    for (int g = lane; g < G; g += 64) t += gsum[g];
+    return rsqrtf(wave_total(t) / static_cast<float>(K) + eps);
+}
+
 // The value of lane l ^ 32.
 __device__ __forceinline__ float lane_xor32(float v, int lane) {
     const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -51,6 +51,8 @@ _SIGNATURES = {
     "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemv_f16": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_f16_configs": ([ctypes.POINTER(_I), _I], _I),
+    "tw4_rms_norm": ([_P, _P, _P, _I, _I, ctypes.c_float, _P], _I),
+    "tw4_add_rms_norm": ([_P, _P, _P, _I, _I, ctypes.c_float, _P], _I),
 }
 
 

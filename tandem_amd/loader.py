@@ -5,15 +5,14 @@ The counterpart of the parts of 12vivi/tandem that put a real AutoAWQ checkpoint
     QuantConfig              quantization_config of config.json      python/tandem/model_config.py:28-43
     load_weights             safetensors -> parameters and AWQ        python/tandem/models/loader.py:14-105
                              buffers, fused q/k/v and gate/up
-    GatedMLP                 gate_up + down with the SwiGLU epilogue  python/tandem/layers/mlp.py:16-45
-                             enabled on the W4 gate_up (TANDEM_W4_FUSE_ACT)
 
 A checkpoint stores q_proj / k_proj / v_proj and gate_proj / up_proj separately; the model holds
 one fused qkv_proj and gate_up_proj. Dense weights are fused along their rows; the AutoAWQ
 tensors (qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N]) carry the output dimension second,
 so they are fused along their columns: shard offsets are taken from the fused size (q first, k and
 v sharing the remainder; gate and up halves). Loading is host work on CPU tensors; the W4Linear
-layers are then moved to the GPU and repacked by ``finalize_quantized``.
+layers are then moved to the GPU and repacked by ``finalize_quantized`` (``tandem_amd.model.prepare``).
+The model classes, with the SwiGLU wiring of the MLP, are in ``tandem_amd.model``.
 """
 
 from __future__ import annotations
@@ -28,7 +27,6 @@ from typing import Any, Optional
 import torch
 from torch import nn
 
-from tandem_amd.layers.linear import make_linear
 
 logger = logging.getLogger(__name__)
 
@@ -132,28 +130,3 @@ def load_weights(model: nn.Module, model_path: str) -> None:
     missing = sorted(set(targets) - loaded)
     if missing:
         raise RuntimeError(f"{len(missing)} parameters missing from checkpoint, e.g. {missing[:5]}")
-
-
-def silu_and_mul(y: torch.Tensor) -> torch.Tensor:
-    """silu(gate) * up on [..., gate | up] (the separate activation of an unfused MLP)."""
-    half = y.shape[-1] // 2
-    return torch.nn.functional.silu(y[..., :half]) * y[..., half:]
-
-
-class GatedMLP(nn.Module):
-    """SwiGLU MLP with one fused gate_up projection (python/tandem/layers/mlp.py:16-45): with an
-    AWQ checkpoint the gate_up W4Linear applies SwiGLU in its kernel epilogue unless
-    TANDEM_W4_FUSE_ACT=0."""
-
-    def __init__(self, hidden_size: int, intermediate_size: int, quant: Optional[QuantConfig] = None) -> None:
-        super().__init__()
-        self.intermediate_size = intermediate_size
-        self.gate_up_proj = make_linear(hidden_size, 2 * intermediate_size, False, quant)
-        self.down_proj = make_linear(intermediate_size, hidden_size, False, quant)
-        enable = getattr(self.gate_up_proj, "enable_silu_mul", None)
-        self.fused_act = bool(enable is not None and os.environ.get("TANDEM_W4_FUSE_ACT", "1") != "0" and enable())
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.fused_act:
-            return self.down_proj(self.gate_up_proj(x))
-        return self.down_proj(silu_and_mul(self.gate_up_proj(x)))

@@ -1,0 +1,208 @@
+"""The decode step around the projections: the norm kernels (tw4_rms_norm / tw4_add_rms_norm)
+against the oracle, a small W4A16 decoder (tandem_amd.model) against a numpy restatement of the
+same step built from the oracle's pieces, and the bucketed HIP-graph runner (tandem_amd.decode_graph)
+against eager runs of the same model (python/tandem/executor/cuda_graph.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as o
+from tandem_amd import decode_graph, model as tmodel
+from tandem_amd.loader import QuantConfig
+
+TINY = tmodel.DecoderConfig(hidden_size=512, intermediate_size=1024, num_heads=4, num_kv_heads=2, head_dim=128,
+                            num_layers=2, vocab_size=1000, rms_norm_eps=1e-6)
+AWQ = QuantConfig("awq", 4, 128)
+
+
+# ------------------------------------------------------------------------------------- CPU
+def test_bucket_sizes():
+    """python/tandem/executor/cuda_graph.py:34-38."""
+    assert decode_graph.bucket_sizes(1) == [1]
+    assert decode_graph.bucket_sizes(3) == [1, 2, 3]
+    assert decode_graph.bucket_sizes(8) == [1, 2, 4, 8]
+    assert decode_graph.bucket_sizes(20) == [1, 2, 4, 8, 16, 20]
+    assert decode_graph.bucket_sizes(32) == [1, 2, 4, 8, 16, 24, 32]
+    with pytest.raises(ValueError):
+        decode_graph.bucket_sizes(0)
+
+
+def test_config_from_hf():
+    hf = {"hidden_size": 4096, "intermediate_size": 12288, "num_attention_heads": 32, "num_key_value_heads": 8,
+          "head_dim": 128, "num_hidden_layers": 36, "vocab_size": 151936, "rms_norm_eps": 1e-6,
+          "tie_word_embeddings": False}
+    assert tmodel.DecoderConfig.from_hf(hf) == tmodel.QWEN3_8B
+
+
+def test_model_parameter_names():
+    """Checkpoint names (python/tandem/models/llama_family.py:1-8) with the fused projections."""
+    with torch.device("meta"):
+        m = tmodel.DecoderModel(TINY, AWQ)
+    names = {n for n, _ in m.named_parameters()} | {n for n, _ in m.named_buffers()}
+    for want in ("model.embed_tokens.weight", "model.norm.weight", "lm_head.weight",
+                 "model.layers.1.self_attn.qkv_proj.qweight", "model.layers.1.self_attn.o_proj.scales",
+                 "model.layers.0.mlp.gate_up_proj.qzeros", "model.layers.0.mlp.down_proj.qweight",
+                 "model.layers.0.input_layernorm.weight", "model.layers.0.post_attention_layernorm.weight"):
+        assert want in names, want
+    assert all(layer.mlp.fused_act for layer in m.model.layers)
+
+
+def test_attend_one_token_is_grouped_value_broadcast():
+    """Softmax over one key is 1: head h's output is the value of KV head h // group."""
+    attn = tmodel.Attention(TINY, None)
+    qkv = torch.randn(3, attn.q_size + 2 * attn.kv_size)
+    out = attn.attend(qkv).view(3, TINY.num_heads, TINY.head_dim)
+    v = qkv[:, attn.q_size + attn.kv_size:].view(3, TINY.num_kv_heads, TINY.head_dim)
+    group = TINY.num_heads // TINY.num_kv_heads
+    for h in range(TINY.num_heads):
+        assert torch.equal(out[:, h], v[:, h // group])
+    q = qkv[:, :attn.q_size].view(3, TINY.num_heads, TINY.head_dim)
+    k = qkv[:, attn.q_size:attn.q_size + attn.kv_size].view(3, TINY.num_kv_heads, TINY.head_dim)
+    for h in range(TINY.num_heads):  # the same through softmax(q k^T / sqrt(d)) v over one key
+        scores = (q[:, h] * k[:, h // group]).sum(-1, keepdim=True) / TINY.head_dim ** 0.5
+        assert torch.allclose(torch.softmax(scores, -1) * v[:, h // group], out[:, h])
+
+
+# ------------------------------------------------------------------------------- GPU helpers
+def _tiny_model(seed: int = 0):
+    """The tiny decoder with oracle-generated AWQ tensors and seeded fp16 parameters; returns the
+    model on the GPU (prepared) and the numpy weights of the step."""
+    rng = np.random.default_rng(seed)
+    m = tmodel.DecoderModel(TINY, AWQ)
+    w = {"layers": []}
+    i = 0
+    for layer in m.model.layers:
+        lw = {}
+        for name, lin in (("qkv", layer.self_attn.qkv_proj), ("o", layer.self_attn.o_proj),
+                          ("gate_up", layer.mlp.gate_up_proj), ("down", layer.mlp.down_proj)):
+            qw, qz, s, _, _ = o.random_awq(lin.in_features, lin.out_features, seed=seed * 100 + i)
+            i += 1
+            lin.qweight.copy_(torch.from_numpy(qw))
+            lin.qzeros.copy_(torch.from_numpy(qz))
+            lin.scales.copy_(torch.from_numpy(s))
+            lw[name] = o.dequant(qw, qz, s)  # fp16 [N, K], the weights the kernels multiply by
+        for name, mod in (("n1", layer.input_layernorm), ("n2", layer.post_attention_layernorm)):
+            v = (1.0 + (rng.random(TINY.hidden_size) - 0.5) * 0.2).astype(np.float16)
+            mod.weight.data = torch.from_numpy(v.astype(np.float32))
+            lw[name] = v
+        w["layers"].append(lw)
+    emb = rng.standard_normal((TINY.vocab_size, TINY.hidden_size)).astype(np.float16)
+    head = (rng.standard_normal((TINY.vocab_size, TINY.hidden_size)) * 0.02).astype(np.float16)
+    fn = (1.0 + (rng.random(TINY.hidden_size) - 0.5) * 0.2).astype(np.float16)
+    m.model.embed_tokens.weight.data = torch.from_numpy(emb.astype(np.float32))
+    m.lm_head.weight.data = torch.from_numpy(head.astype(np.float32))
+    m.model.norm.weight.data = torch.from_numpy(fn.astype(np.float32))
+    w.update(emb=emb, head=head, norm=fn)
+    dev = torch.device("cuda", 0)
+    tmodel.prepare(m, dev, torch.cuda.get_device_name(dev))
+    return m, w
+
+
+def _oracle_step(w, ids) -> np.ndarray:
+    """The decode step restated with the oracle's norms and float64 products, rounded to fp16
+    where the GPU path stores fp16 (python/tandem/models/llama_family.py:47-67, 90-116)."""
+    eps = TINY.rms_norm_eps
+    hidden = w["emb"][ids]
+    residual = None
+    q_size, kv = TINY.num_heads * TINY.head_dim, TINY.num_kv_heads * TINY.head_dim
+    group = TINY.num_heads // TINY.num_kv_heads
+    for lw in w["layers"]:
+        if residual is None:
+            residual = hidden
+            hidden = o.rms_norm(hidden, lw["n1"], eps)
+        else:
+            hidden, residual = o.add_rms_norm(hidden, residual, lw["n1"], eps)
+        qkv = o.linear(hidden, lw["qkv"]).astype(np.float16)
+        v = qkv[:, q_size + kv:].reshape(len(ids), TINY.num_kv_heads, 1, TINY.head_dim)
+        attn = np.broadcast_to(v, (len(ids), TINY.num_kv_heads, group, TINY.head_dim)).reshape(len(ids), q_size)
+        hidden = o.linear(attn, lw["o"]).astype(np.float16)
+        hidden, residual = o.add_rms_norm(hidden, residual, lw["n2"], eps)
+        gu = o.linear(hidden, lw["gate_up"])
+        hidden = o.silu_and_mul(gu).astype(np.float16)
+        hidden = o.linear(hidden, lw["down"]).astype(np.float16)
+    hidden, _ = o.add_rms_norm(hidden, residual, w["norm"], eps)
+    return o.linear(hidden, w["head"])
+
+
+def _close(y: torch.Tensor, ref: np.ndarray, rtol: float, what) -> None:
+    got = y.detach().float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-6)
+    cos = (got * ref).sum() / np.sqrt((got * got).sum() * (ref * ref).sum())
+    assert err <= rtol and cos >= 0.9999, (what, err, cos)
+
+
+# ----------------------------------------------------------------------------------- GPU
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [512, 1024, 2048, 2560, 3584, 4096, 5120, 8192])
+def test_norm_kernels_match_oracle(k):
+    """Residual bit-exact; normalised output within one fp16 ulp of the oracle's float64 result
+    (the kernel's fp32 sum and two fp32 products round differently near ties)."""
+    from tandem_amd.layers import norm
+
+    rng = np.random.default_rng(k)
+    for m in (1, 3, 4, 5, 9):
+        x = (rng.standard_normal((m, k)) * 3).astype(np.float16)
+        r = (rng.standard_normal((m, k)) * 20).astype(np.float16)
+        w = (rng.random(k) + 0.5).astype(np.float16)
+        eps = 1e-6
+        xg, rg, wg = (torch.from_numpy(a).cuda() for a in (x, r, w))
+        y = norm.rms_norm(xg, wg, eps).cpu().numpy()
+        ref = o.rms_norm(x, w, eps)
+        assert (np.abs(y.astype(np.float32) - ref.astype(np.float32)) <= np.spacing(np.abs(ref)).astype(np.float32)).all()
+        yx, rx = norm.fused_add_rms_norm(xg, rg, wg, eps)
+        assert yx.data_ptr() == xg.data_ptr() and rx.data_ptr() == rg.data_ptr()  # in place
+        ref_y, ref_r = o.add_rms_norm(x, r, w, eps)
+        assert (rg.cpu().numpy().view(np.uint16) == ref_r.view(np.uint16)).all()
+        got = xg.cpu().numpy()
+        assert (np.abs(got.astype(np.float32) - ref_y.astype(np.float32))
+                <= np.spacing(np.abs(ref_y)).astype(np.float32)).all(), (k, m)
+
+
+@pytest.mark.gpu
+def test_norm_zero_rows_and_errors():
+    from tandem_amd.layers import norm
+
+    w = torch.ones(1024, dtype=torch.float16, device="cuda")
+    x = torch.zeros(2, 1024, dtype=torch.float16, device="cuda")
+    assert (norm.rms_norm(x, w, 1e-6) == 0).all()
+    assert norm.rms_norm(x[:0], w, 1e-6).shape == (0, 1024)
+    with pytest.raises(RuntimeError, match="K % 512"):
+        norm.rms_norm(torch.zeros(1, 1000, dtype=torch.float16, device="cuda"),
+                      torch.ones(1000, dtype=torch.float16, device="cuda"), 1e-6)
+
+
+@pytest.mark.gpu
+def test_tiny_decoder_step_matches_oracle():
+    model, w = _tiny_model(seed=1)
+    for ids in ([7], [3, 999], [1, 2, 3, 4, 5], list(range(20, 44))):
+        logits = model.compute_logits(model(torch.tensor(ids, device="cuda")))
+        assert logits.shape == (len(ids), TINY.vocab_size) and logits.dtype == torch.float16
+        _close(logits, _oracle_step(w, np.array(ids)), 0.02, ids)
+
+
+@pytest.mark.gpu
+def test_graph_runner_matches_eager_buckets():
+    """Each bucket's replay equals the eager step on the same padded batch, bit for bit, and stays
+    so over repeated replays with eager work and synchronisations in between."""
+    model, w = _tiny_model(seed=2)
+    runner = decode_graph.DecodeGraphRunner(model, max_bs=8, device=torch.device("cuda", 0))
+    assert runner.sizes == [1, 2, 4, 8]
+    rng = np.random.default_rng(0)
+    for rep in range(3):
+        for b in (1, 2, 3, 5, 8):
+            ids = rng.integers(0, TINY.vocab_size, size=b)
+            got = runner.run(ids.tolist()).clone()
+            bs = runner.bucket(b)
+            padded = torch.zeros(bs, dtype=torch.long, device="cuda")
+            padded[:b] = torch.from_numpy(ids).cuda()
+            with torch.inference_mode():
+                eager = model.compute_logits(model(padded))[:b]
+            torch.cuda.synchronize()
+            assert torch.equal(got, eager), (rep, b)
+            if rep == 0:
+                _close(got, _oracle_step(w, ids), 0.02, ("runner", b))
+    with pytest.raises(ValueError):
+        runner.run(list(range(9)))

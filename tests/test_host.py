@@ -78,6 +78,10 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_gemv_act(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 24, 128, 4, 2, 1, 1, None),
          "SwiGLU"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 65, 64, 128, 4, 2, 1, 0, None), "M <= 64"),
+        (lambda: lib.tw4_rms_norm(_fake(), _fake(), _fake(), 1, 1000, 1e-6, None), "K % 512"),
+        (lambda: lib.tw4_rms_norm(_fake(), _fake(), _fake(), 1, 16384, 1e-6, None), "K <= 8192"),
+        (lambda: lib.tw4_add_rms_norm(_fake(4104), _fake(), _fake(), 1, 1024, 1e-6, None), "aligned"),
+        (lambda: lib.tw4_add_rms_norm(_fake(), None, _fake(), 1, 1024, 1e-6, None), "null"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
                               32, 64, 128, 2, 1, 4, 1, 2, 17, 0, None), "splits"),

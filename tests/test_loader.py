@@ -14,7 +14,7 @@ from safetensors.torch import save_file
 from torch import nn
 
 from oracle import awq_oracle as o
-from tandem_amd import loader
+from tandem_amd import loader, model as tmodel
 from tandem_amd.layers import linear
 
 H, I, Q, KV = 256, 384, 256, 128  # hidden, intermediate, q and k / v output sizes
@@ -31,7 +31,7 @@ class Layer(nn.Module):
     def __init__(self, quant):
         super().__init__()
         self.self_attn = Attn(quant)
-        self.mlp = loader.GatedMLP(H, I, quant)
+        self.mlp = tmodel.GatedMLP(H, I, quant)
         self.input_layernorm = nn.LayerNorm(H)
 
 

@@ -210,3 +210,90 @@ def test_planted_mistakes_are_caught():
     t = np.arange(32)[:, None]
     swapped = o.interleave_gate_up(np.concatenate([t[16:], t[:16]]))
     assert not (swapped == o.interleave_gate_up(t)).all()
+
+
+# ------------------------------------------- norms (ops.py:107-120, triton_ops.py:101-124)
+def _norm_constant_row_expected(c: float, w: float, eps: float) -> np.float16:
+    """A row of K equal values c: mean(x^2) = c^2 for any K, so y = c / sqrt(c^2 + eps) * w."""
+    return np.float16(c / np.sqrt(c * c + eps) * w)
+
+
+@pytest.mark.parametrize("c", [1.0, -3.5, 0.0078125, 1000.0])
+@pytest.mark.parametrize("k", [512, 4096])
+def test_rms_norm_constant_row(c, k):
+    w = np.full(k, 0.75, dtype=np.float16)
+    y = o.rms_norm(np.full((1, k), c, dtype=np.float16), w, 1e-6)
+    assert (y == _norm_constant_row_expected(c, 0.75, 1e-6)).all()
+
+
+def test_rms_norm_zero_row_and_eps():
+    """eps keeps a zero row finite; with x^2 << eps, y = x / sqrt(eps) * w (eps dominates)."""
+    k, eps = 512, 1e-2
+    w = np.ones(k, dtype=np.float16)
+    assert (o.rms_norm(np.zeros((2, k), dtype=np.float16), w, eps) == 0).all()
+    x = np.full((1, k), 2.0 ** -10, dtype=np.float16)
+    assert o.rms_norm(x, w, eps)[0, 0] == np.float16(2.0 ** -10 / np.sqrt(2.0 ** -20 + eps))
+
+
+def test_rms_norm_explicit_loops():
+    rng = np.random.default_rng(5)
+    k = 512
+    x = rng.standard_normal((3, k)).astype(np.float16)
+    w = (rng.random(k) + 0.5).astype(np.float16)
+    y = o.rms_norm(x, w, 1e-6)
+    for m in range(3):
+        row = [float(v) for v in x[m]]
+        rstd = 1.0 / np.sqrt(sum(v * v for v in row) / k + 1e-6)
+        want = np.array([row[i] * rstd * float(w[i]) for i in range(k)]).astype(np.float16)
+        assert (np.abs(y[m].astype(np.float32) - want.astype(np.float32))
+                <= np.spacing(np.abs(want)).astype(np.float32)).all()
+
+
+def test_add_rms_norm_residual_and_sum():
+    """r' = fp16(fp32(x + r)) element by element; y is the norm of the fp32 sum: equal to rms_norm
+    of s where s is exact in fp16, and a scale-free function of the row (powers of two)."""
+    rng = np.random.default_rng(6)
+    k = 1024
+    x = rng.standard_normal((2, k)).astype(np.float16)
+    r = rng.standard_normal((2, k)).astype(np.float16)
+    w = (rng.random(k) + 0.5).astype(np.float16)
+    y, r2 = o.add_rms_norm(x, r, w, 1e-6)
+    for m in range(2):
+        for i in range(0, k, 37):
+            assert r2[m, i] == np.float16(np.float32(float(x[m, i])) + np.float32(float(r[m, i])))
+    xs = (x.astype(np.float32) * 0.5).astype(np.float16)  # x / 2 and x / 2: s = x exactly
+    y2, r3 = o.add_rms_norm(xs, xs, w, 0.0)
+    assert (r3 == x).all() and (y2 == o.rms_norm(x, w, 0.0)).all()
+    y4, _ = o.add_rms_norm(xs * np.float16(4), xs * np.float16(4), w, 0.0)  # s = 4 x
+    assert (y4 == y2).all()
+
+
+def _add_rms_norm_no_residual(x, r, w, eps):  # forgets to add the residual into the normalised value
+    return o.rms_norm(x, w, eps), (x.astype(np.float32) + r.astype(np.float32)).astype(np.float16)
+
+
+def _rms_norm_unbiased(x, w, eps):  # mean over K - 1
+    x64 = x.astype(np.float64)
+    rstd = 1.0 / np.sqrt((x64 * x64).sum(-1, keepdims=True) / (x.shape[-1] - 1) + eps)
+    return (x64 * rstd * w.astype(np.float64)).astype(np.float16)
+
+
+def _rms_norm_no_eps(x, w, eps):
+    x64 = x.astype(np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return (x64 / np.sqrt(np.mean(x64 * x64, -1, keepdims=True)) * w.astype(np.float64)).astype(np.float16)
+
+
+def test_planted_norm_mistakes_are_caught():
+    k = 512
+    w = np.full(k, 0.75, dtype=np.float16)
+    row = np.full((1, k), 1.0, dtype=np.float16)
+    assert not (_rms_norm_unbiased(row, w, 1e-6) == _norm_constant_row_expected(1.0, 0.75, 1e-6)).all()
+    assert not (_rms_norm_no_eps(np.zeros((1, k), dtype=np.float16), w, 1e-2) == 0).all()
+    x = np.full((1, k), 0.5, dtype=np.float16)
+    r = np.full((1, k), -2.0, dtype=np.float16)
+    y_bad, _ = _add_rms_norm_no_residual(x, r, w, 1e-6)
+    assert (y_bad == _norm_constant_row_expected(0.5, 0.75, 1e-6)).all()
+    assert not (y_bad == _norm_constant_row_expected(-1.5, 0.75, 1e-6)).all()  # the true s = -1.5
+    y, _ = o.add_rms_norm(x, r, w, 1e-6)
+    assert (y == _norm_constant_row_expected(-1.5, 0.75, 1e-6)).all()
