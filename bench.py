@@ -21,6 +21,9 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
   full_stack    the whole decode step of the linears plus the fp16 lm_head (4096 x 151936, through
                 layers/gemv16.py's table: the HIP fp16 GEMV where it has an entry, else F.linear),
                 M in {1, 8, 32}: us per step and GB/s
+  decode_step   the model's decode step (tandem_amd.model: norms, one-token attention, SwiGLU
+                gate_up, lm_head) replayed from the bucketed HIP graphs of tandem_amd.decode_graph,
+                M in {1, 8, 32}: us per step, tokens/s, GB/s of the step's weight bytes
 """
 
 from __future__ import annotations
@@ -110,7 +113,7 @@ def kernel_of(awq, lin, m: int) -> str:
     if m <= 16:
         key = (lin.out_features, lin.in_features, m)
         kind = (lin.kernels.get((*key, "silu")) if lin.silu_mul else None) or lin.kernels.get(key, awq.DEFAULT_KERNEL)
-        if kind[0] == "gemv" and (m > 4 or lin.silu_mul):
+        if kind[0] == "gemv" and m > 4:
             kind = awq.DEFAULT_KERNEL
         return f"{kind[0]}{tuple(kind[1:])}"
     key = (lin.out_features, lin.in_features) + (("silu",) if lin.silu_mul else ())
@@ -158,6 +161,45 @@ def cpu_baseline(budget_s: float, m: int) -> dict:
                       f"AWQ unpack + fp16 dequant + float32 BLAS matmul per call, BLAS on {threads} threads "
                       f"(dequant single-threaded); {t_total:.1f} s; host {model} ({cores} cores visible)",
             "ms_per_layer": round(t_total / done * 1e3, 2)}
+
+
+def decode_step(torch, dev) -> dict:
+    """The whole Qwen3-8B decode step of tandem_amd.model (embedding, 36 x {add + RMSNorm, qkv,
+    one-token attention, o, add + RMSNorm, gate_up with SwiGLU, down}, final add + RMSNorm, fp16
+    lm_head) replayed from tandem_amd.decode_graph's bucket graphs, random AWQ weights."""
+    from tandem_amd import decode_graph, model as tmodel
+    from tandem_amd.loader import QuantConfig
+
+    cfg = tmodel.QWEN3_8B
+    with torch.device(dev):
+        mdl = tmodel.DecoderModel(cfg, QuantConfig("awq", 4, 128))
+    mdl.half()
+    tmodel.init_random(mdl, seed=7)
+    tmodel.prepare(mdl, dev, torch.cuda.get_device_name(dev))
+    runner = decode_graph.DecodeGraphRunner(mdl, max_bs=32, device=dev)
+    h, i, v = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qkv_n = (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
+    out = {}
+    for bs in (1, 8, 32):
+        runner.run(list(range(bs)))
+        graph = runner.graphs[bs]
+        cur = torch.cuda.current_stream(dev)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            graph.replay()
+        t0.record(cur)
+        for _ in range(20):
+            graph.replay()
+        t1.record(cur)
+        t1.synchronize()
+        us = t0.elapsed_time(t1) / 20 * 1e3
+        b = cfg.num_layers * (call_bytes(bs, h, qkv_n) + call_bytes(bs, cfg.num_heads * cfg.head_dim, h)
+                              + call_bytes(bs, h, 2 * i) - bs * 2 * i + call_bytes(bs, i, h)) + 2 * v * h
+        out[f"m{bs}"] = {"us_per_step": round(us, 1), "tokens_per_s": round(bs / us * 1e6, 1),
+                         "GBps": round(b / us / 1e3, 1), "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1)}
+    del runner, mdl
+    torch.cuda.synchronize()
+    return out
 
 
 def main() -> int:
@@ -266,6 +308,8 @@ def main() -> int:
         del head
         torch.cuda.synchronize()
 
+    step = {} if a.no_detail else decode_step(torch, dev)
+
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds, m)
     line = {
         "metric": "W4A16 us/call + achieved HBM GB/s (% peak), Qwen3-8B shapes, M=1/8/32",
@@ -278,7 +322,7 @@ def main() -> int:
                    "step_bytes": step_bytes, "step_flops": step_flops},
         "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
         "us_per_layer": round(step_s / a.layers * 1e6, 2),
-        "roofline": roofline, "cpu_baseline": cpu, "detail": detail, "full_stack": full,
+        "roofline": roofline, "cpu_baseline": cpu, "detail": detail, "full_stack": full, "decode_step": step,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(line), flush=True)

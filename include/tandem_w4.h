@@ -96,6 +96,21 @@ int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scale
                  const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                  int warps_k, int unroll, int ntile, int act, void* stream);
 
+/* The decoder layer's add + RMSNorm fused into a decode kernel's x staging: the kernel
+ * (kind 0: tw4_gemv_act, 1 <= M <= 4; kind 1: tw4_mma with x in LDS, 1 <= M <= 16 and
+ * M (K + 8) 2 <= 80 KB) runs on a = fp16((x + residual) * rsqrt(mean((x + residual)^2) + eps)
+ * * norm_weight), the fp32 sum s = x + residual, and writes residual_out = fp16(s) (not in
+ * place). residual = NULL: plain RMSNorm of x, residual_out unused. y and residual_out are
+ * bit-identical to tw4_add_rms_norm (or tw4_rms_norm) followed by the same kernel and config.
+ * norm_weight fp16 [K]; x, residual, residual_out fp16 [M, K], 16-byte aligned.
+ * Replaces the unfused pair ops.fused_add_rms_norm + projection of the reference's decoder layer
+ * (python/tandem/models/llama_family.py:58-65; its fused-prologue GEMV,
+ * python/tandem/layers/triton_gemv.py:92-178, 330-415, is the same idea for fp16 weights). */
+int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
+                    const uint16_t* norm_weight, float eps, const int32_t* packed,
+                    const uint16_t* scales, const uint16_t* zeros, uint16_t* y, int M, int N,
+                    int K, int kind, int warps_k, int unroll, int ntile, int act, void* stream);
+
 /* Decode on the matrix cores (v_mfma_f32_16x16x32_f16, weights as the A operand, the batch on
  * the 16-column side, ceil(M / 16) column tiles), 1 <= M <= 64; unroll * ceil(M / 16) <= 4.
  * act = 1: y = silu(gate) * up, [M, N/2], rows in interleave_gate_up order (N % 16 == 0);

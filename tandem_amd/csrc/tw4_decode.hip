@@ -83,19 +83,22 @@ __device__ __forceinline__ TileStreams<NT> tile_streams(const u4* w, const uint1
     return ts;
 }
 
-// LDS layout of a decode workgroup (offsets in 16-byte units): [x rows][corr][reduction].
+// LDS layout of a decode workgroup (offsets in 16-byte units): [x rows][corr][norm][reduction].
 struct DecodeLds {
     int xs;    // x row stride (u4): K / 8 + 1
     int corr;  // gemv: per (m, group, slice) sums of x' and x (float2)
+    int norm;  // fused norm prologue: per (m, group) sums of squares (float [M][G])
     int red;   // cross-wavefront reduction
     int total;
 };
 
-__host__ __device__ __forceinline__ DecodeLds decode_lds(bool xlds, int M, int K, int corr_u4, int red_u4) {
+__host__ __device__ __forceinline__ DecodeLds decode_lds(bool xlds, int M, int K, int corr_u4, int red_u4,
+                                                         bool norm = false) {
     DecodeLds l;
     l.xs = (K >> 3) + 1;
     l.corr = xlds ? M * l.xs : 0;
-    l.red = l.corr + corr_u4;
+    l.norm = l.corr + corr_u4;
+    l.red = l.norm + (norm ? (M * (K >> 7) + 3) / 4 : 0);
     l.total = l.red + red_u4;
     return l;
 }
@@ -145,9 +148,12 @@ struct XSlice {
     uint32_t magic;  // ceil(2^32 / n16): f / n16 == umulhi(f, magic) for f < 16 n16 <= 2^17 (K <= 65536)
 };
 
+// An empty slice (gb == ge == G) gets c0 = 0, so the unconditional loads of the fused norm
+// prologue read chunk 0 of row 0 (16 gb would be one chunk past the end of x and of the weight).
 __device__ __forceinline__ XSlice x_slice(int gb, int ge, int M) {
     const int n16 = 16 * (ge - gb);
-    return XSlice{16 * gb, n16, M * n16, n16 > 0 ? static_cast<uint32_t>(0xFFFFFFFFu / static_cast<uint32_t>(n16)) + 1u : 0u};
+    return XSlice{n16 > 0 ? 16 * gb : 0, n16, M * n16,
+                  n16 > 0 ? static_cast<uint32_t>(0xFFFFFFFFu / static_cast<uint32_t>(n16)) + 1u : 0u};
 }
 
 struct XPos {
@@ -155,10 +161,10 @@ struct XPos {
 };
 
 // Flat chunk f -> (row, chunk in row); f past the slice -> its last chunk. ONE_ROW: M == 1 known at
-// compile time, no division.
+// compile time, no division (magic is 0 for an empty slice, so m = 0 there too).
 template <bool ONE_ROW>
 __device__ __forceinline__ XPos x_pos(const XSlice& xs, int f) {
-    f = min(f, xs.n - 1);
+    f = max(min(f, xs.n - 1), 0);  // an empty slice (n = 0) reads chunk 0 of row 0: a valid address
     if constexpr (ONE_ROW) return XPos{0, f};
     const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(f), xs.magic));
     return XPos{m, f - m * xs.n16};
@@ -229,6 +235,139 @@ __device__ __forceinline__ void stage_x(u4* smem, const DecodeLds& l, float2* co
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Fused norm prologue: x is replaced by a = fp16(s rstd w) with s = x + r (fp32; r = 0 without a
+// residual) and rstd = rsqrt(mean(s^2) + eps) over the whole row, the bits tw4_add_rms_norm /
+// tw4_rms_norm would write, then staged as above. The workgroup's wavefronts together cover every
+// quant group of K, so each adds its slice's group sums of squares (norm_rstd's order: sumsq8 per
+// chunk, row16_sum over the 16 chunks of a group, held by lanes 16 i .. 16 i + 15 of one batch)
+// into LDS, and after one workgroup barrier every wavefront reads all G sums of a row. Workgroup 0
+// writes the residual sum fp16(s) to r_out after its main loop (never in place: other workgroups
+// still read r). Every load up to the end of staging is unconditional (a missing residual is read
+// as x and not added; an empty slice reads chunk 0) and no store is issued, so each wait for x
+// counts exactly and never waits for the weight chunk issued behind it.
+struct NormIn {
+    const h1* r;  // residual [M, K], or null: plain RMSNorm of x
+    h1* r_out;    // fp16(x + r) [M, K] (when r)
+    const h1* w;  // norm weight [K]
+    float eps;
+};
+
+constexpr int kNormMaxRows = 16;
+
+__device__ __forceinline__ void norm_sum(const u4& xv, const u4& rv, bool has_r, float (&s)[8]) {
+    chunk_to_f32(xv, s);
+    if (has_r) {
+        float b[8];
+        chunk_to_f32(rv, b);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] += b[i];
+    }
+}
+
+// rg: the residual, or x itself when there is none (loaded, not added).
+template <bool ONE_ROW, bool W>
+__device__ __forceinline__ void load_norm_batch(u4 (&xv)[kXB], u4 (&rv)[kXB], u4 (&wv)[kXB], const u4* xg,
+                                                const u4* rg, const u4* wg, int kx, const XSlice& xs, int f0) {
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) {
+        const XPos p = x_pos<ONE_ROW>(xs, f0 + 64 * j);
+        xv[j] = x_chunk(xg, kx, xs, p);
+        rv[j] = x_chunk(rg, kx, xs, p);
+        if constexpr (W) wv[j] = wg[xs.c0 + p.c];
+    }
+}
+
+template <bool ONE_ROW>
+__device__ __forceinline__ void norm_group_sums(float* gsum, const u4 (&xv)[kXB], const u4 (&rv)[kXB], bool has_r,
+                                                const XSlice& xs, int G, int f0, int lane) {
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) {
+        float sv[8];
+        norm_sum(xv[j], rv[j], has_r, sv);
+        const float q = row16_sum(sumsq8(sv));
+        const int f = f0 + 64 * j;
+        const XPos p = x_pos<ONE_ROW>(xs, f);
+        if ((lane & 15) == 0 && f < xs.n) gsum[p.m * G + ((xs.c0 + p.c) >> 4)] = q;
+    }
+}
+
+template <bool BIASED, bool ONE_ROW, int MR>
+__device__ __forceinline__ void norm_store_batch(u4* smem, const DecodeLds& l, float2* corr, int kx, const XSlice& xs,
+                                                 const u4 (&xv)[kXB], const u4 (&rv)[kXB], const u4 (&wv)[kXB],
+                                                 bool has_r, const float (&rstd)[MR], int f0) {
+#pragma unroll
+    for (int j = 0; j < kXB; ++j) {
+        const int f = f0 + 64 * j;
+        const XPos p = x_pos<ONE_ROW>(xs, f);
+        float sv[8], gv[8];
+        norm_sum(xv[j], rv[j], has_r, sv);
+        float rs = rstd[0];
+#pragma unroll
+        for (int m = 1; m < MR; ++m) rs = p.m == m ? rstd[m] : rs;
+        chunk_to_f32(wv[j], gv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sv[i] = sv[i] * rs * gv[i];
+        store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, f32_to_chunk(sv), f);
+    }
+}
+
+// Called by every wavefront of the workgroup (it holds a workgroup barrier); a wavefront with an
+// empty slice only takes part in the barrier. fx / fr / fw: the slice's first batch, already loaded.
+template <bool BIASED, bool ONE_ROW, int MR>
+__device__ __forceinline__ void stage_x_norm(u4* smem, const DecodeLds& l, float2* corr, const u4* xg, int kx,
+                                             const XSlice& xs, const NormIn& nin, int M, int G, int K,
+                                             const u4 (&fx)[kXB], const u4 (&fr)[kXB], const u4 (&fw)[kXB],
+                                             int lane) {
+    float* gsum = reinterpret_cast<float*>(smem + l.norm);  // [M][G]
+    const bool has_r = nin.r != nullptr;
+    const u4* rg = has_r ? reinterpret_cast<const u4*>(nin.r) : xg;
+    const u4* wg = reinterpret_cast<const u4*>(nin.w);
+    if (xs.n > 0) {
+        norm_group_sums<ONE_ROW>(gsum, fx, fr, has_r, xs, G, lane, lane);
+        for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {  // wavefront-uniform trip count
+            u4 xv[kXB], rv[kXB], wv[kXB];
+            load_norm_batch<ONE_ROW, false>(xv, rv, wv, xg, rg, wg, kx, xs, f0);
+            norm_group_sums<ONE_ROW>(gsum, xv, rv, has_r, xs, G, f0, lane);
+        }
+    }
+    __syncthreads();
+    float rstd[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        rstd[m] = m < M ? norm_rstd(gsum + m * G, G, K, nin.eps, lane) : 0.0f;  // wavefront-uniform branch
+    if (xs.n > 0) {
+        norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, fx, fr, fw, has_r, rstd, lane);
+        for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {
+            u4 xv[kXB], rv[kXB], wv[kXB];
+            load_norm_batch<ONE_ROW, true>(xv, rv, wv, xg, rg, wg, kx, xs, f0);
+            norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, xv, rv, wv, has_r, rstd, f0);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Workgroup 0, after its main loop: fp16(x + r) of the wavefront's slice into r_out.
+template <bool ONE_ROW>
+__device__ __forceinline__ void write_residual(const u4* xg, const NormIn& nin, int kx, const XSlice& xs, int lane) {
+    if (nin.r == nullptr || blockIdx.x != 0) return;
+    const u4* rg = reinterpret_cast<const u4*>(nin.r);
+    u4* rog = reinterpret_cast<u4*>(nin.r_out);
+    for (int f0 = lane; f0 - lane < xs.n; f0 += 64 * kXB) {
+        u4 xv[kXB], rv[kXB], wv[kXB];
+        load_norm_batch<ONE_ROW, false>(xv, rv, wv, xg, rg, nullptr, kx, xs, f0);
+#pragma unroll
+        for (int j = 0; j < kXB; ++j) {
+            const int f = f0 + 64 * j;
+            const XPos p = x_pos<ONE_ROW>(xs, f);
+            float sv[8];
+            norm_sum(xv[j], rv[j], true, sv);
+            if (f < xs.n) rog[static_cast<int64_t>(p.m) * kx + xs.c0 + p.c] = f32_to_chunk(sv);
+        }
+    }
+}
+
 __device__ __forceinline__ GroupQ group_q_raw(uint32_t s, uint32_t z, bool valid) {
     return group_q(valid ? as_h1(s) : static_cast<h1>(0.0f), as_h1(z));
 }
@@ -288,16 +427,16 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
     }
 }
 
-template <int M, int WK, int U, int NT>
+template <int M, int WK, int U, int NT, bool NORM>
 __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                       const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                      h1* __restrict__ y, int N, int K, int act) {
+                                                      h1* __restrict__ y, int N, int K, int act, NormIn nin) {
     extern __shared__ u4 smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
     const int tile0 = blockIdx.x * NT;
-    const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, NT));
+    const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, NT), NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
@@ -310,7 +449,15 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const u4* xg = reinterpret_cast<const u4*>(x);
     const XSlice xsl = x_slice(gb, ge, M);
     WeightSet<U, NT> a, b;
-    if (nch > 0) {
+    if constexpr (NORM) {  // no branch around these loads (see stage_x_norm); ge - 1 >= 0 is a valid group
+        u4 fx[kXB], fr[kXB], fw[kXB];
+        load_norm_batch<M == 1, true>(fx, fr, fw, xg, nin.r ? reinterpret_cast<const u4*>(nin.r) : xg,
+                                      reinterpret_cast<const u4*>(nin.w), kx, xsl, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        stage_x_norm<true, M == 1, M>(smem, l, corr, xg, kx, xsl, nin, M, G, K, fx, fr, fw, lane);
+    } else if (nch > 0) {
         u4 xfirst[kXB];
         load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
         __builtin_amdgcn_sched_barrier(0);
@@ -336,6 +483,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     } else if (i + 1 == nch) {
         gemv_chunk<false, M, U, NT>(a, b, ts, s16, z16, smem, corr, l, acc, gb + U * i, ge, G, kb, magic);
     }
+    if constexpr (NORM) write_residual<M == 1>(xg, nin, kx, xsl, lane);
     // lanes r, r + 16, r + 32, r + 48 hold the four k slices of row r
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -439,11 +587,12 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
     }
 }
 
-template <int WK, int U, int NT, int MT, bool XLDS>
+template <int WK, int U, int NT, int MT, bool XLDS, bool NORM = false>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                     h1* __restrict__ y, int M, int N, int K, int act) {
+                                                     h1* __restrict__ y, int M, int N, int K, int act, NormIn nin) {
     static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
+    static_assert(!NORM || XLDS, "the fused norm stages x in LDS");
     if constexpr (U * MT > 4 && MT > 1) {
         return;  // register budget: never launched (tw4_mma rejects U * MT > 4 for M > 16)
     } else {
@@ -452,7 +601,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
     const int tile0 = blockIdx.x * NT;
-    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * MT * 64);
+    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * MT * 64, NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
@@ -466,11 +615,19 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int nch = (ge - gb + U - 1) / U;
 
     WeightSet<U, NT> a, b;
+    const int kx = K >> 3;
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    const XSlice xsl = x_slice(gb, ge, M);
     if constexpr (XLDS) {
-        const int kx = K >> 3;
-        const u4* xg = reinterpret_cast<const u4*>(x);
-        const XSlice xsl = x_slice(gb, ge, M);
-        if (nch > 0) {
+        if constexpr (NORM) {  // no branch around these loads (see stage_x_norm)
+            u4 fx[kXB], fr[kXB], fw[kXB];
+            load_norm_batch<false, true>(fx, fr, fw, xg, nin.r ? reinterpret_cast<const u4*>(nin.r) : xg,
+                                         reinterpret_cast<const u4*>(nin.w), kx, xsl, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
+            __builtin_amdgcn_sched_barrier(0);
+            stage_x_norm<false, false, kNormMaxRows>(smem, l, nullptr, xg, kx, xsl, nin, M, G, K, fx, fr, fw, lane);
+        } else if (nch > 0) {
             u4 xfirst[kXB];
             load_x_batch<false>(xfirst, xg, kx, xsl, lane);
             __builtin_amdgcn_sched_barrier(0);
@@ -498,6 +655,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     } else if (i + 1 == nch) {
         mma_chunk<false, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
     }
+    if constexpr (NORM) write_residual<false>(xg, nin, kx, xsl, lane);
     if (WK > 1) {
         f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][MT][64]
         if (wave > 0) {
@@ -578,17 +736,22 @@ int decode_prepare(int dev) {
     }
     if (g_decode_ready[dev]) return TW4_OK;
     int rc = TW4_OK;
+#define TW4_ATTR_GEMV(WK, U, T, NORM)                                        \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<1, WK, U, T, NORM>);        \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<2, WK, U, T, NORM>);        \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<3, WK, U, T, NORM>);        \
+    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<4, WK, U, T, NORM>);
 #define TW4_ATTR(WK, U, T)                                                   \
-    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<1, WK, U, T>);              \
-    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<2, WK, U, T>);              \
-    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<3, WK, U, T>);              \
-    if (rc == TW4_OK) rc = allow_lds(gemv_kernel<4, WK, U, T>);              \
+    TW4_ATTR_GEMV(WK, U, T, false)                                           \
+    TW4_ATTR_GEMV(WK, U, T, true)                                            \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true>);         \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true, true>);   \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, false>);        \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, false>);        \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, false>);
     TW4_DECODE_CONFIGS(TW4_ATTR)
 #undef TW4_ATTR
+#undef TW4_ATTR_GEMV
     if (rc == TW4_OK) g_decode_ready[dev] = 1;
     return rc;
 }
@@ -601,16 +764,17 @@ int ensure_prepared() {
     return decode_prepare(dev);
 }
 
-template <int M>
+template <int M, bool NORM>
 int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
-                  int act, hipStream_t st) {
+                  int act, const NormIn& nin, hipStream_t st) {
     const int tiles = (N + 15) >> 4;
 #define TW4_GEMV_CASE(WK, U, T)                                                                              \
     if (wk == WK && un == U && nt == T) {                                                                    \
-        const size_t lds = 16 * static_cast<size_t>(decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, T)).total); \
+        const size_t lds =                                                                                   \
+            16 * static_cast<size_t>(decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, T), NORM).total); \
         TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
-                    "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);          \
-        gemv_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act);       \
+                    "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);                                 \
+        gemv_kernel<M, WK, U, T, NORM><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act, nin); \
         TW4_LAUNCH_CHECK("gemv: launch");                                                                    \
         return TW4_OK;                                                                                       \
     }
@@ -654,11 +818,12 @@ extern "C" int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint
     auto zp = reinterpret_cast<const h1*>(zeros);
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
+    const NormIn none{nullptr, nullptr, nullptr, 0.0f};
     switch (M) {
-        case 1: return gemv_dispatch<1>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        case 2: return gemv_dispatch<2>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        case 3: return gemv_dispatch<3>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        default: return gemv_dispatch<4>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        case 1: return gemv_dispatch<1, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
+        case 2: return gemv_dispatch<2, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
+        case 3: return gemv_dispatch<3, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
+        default: return gemv_dispatch<4, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
     }
 }
 
@@ -667,6 +832,45 @@ extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t
     return tw4_gemv_act(x, packed, scales, zeros, y, M, N, K, warps_k, unroll, ntile, 0, stream);
 }
 
+namespace tw4 {
+
+// One mma launch; nin (not null): the fused norm prologue, which needs x in LDS.
+int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, int M, int N, int K, int warps_k,
+               int unroll, int ntile, int act, const NormIn* nin, hipStream_t st) {
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    TW4_REQUIRE(mt == 1 || unroll * mt <= 4, TW4_ECONFIG,
+                "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
+    const int tiles = (N + 15) >> 4;
+    const bool xlds = mt == 1 && static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+    TW4_REQUIRE(!nin || xlds, TW4_ECONFIG,
+                "mma: the fused norm stages x in LDS: M (K + 8) 2 bytes <= %d (M = %d, K = %d)", kXLdsLimit, M, K);
+    const NormIn none{nullptr, nullptr, nullptr, 0.0f};
+#define TW4_MMA_CASE(WK, U, T)                                                                                 \
+    if (warps_k == WK && unroll == U && ntile == T) {                                                          \
+        const size_t lds =                                                                                     \
+            16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * mt * 64, nin != nullptr).total); \
+        const unsigned grid = (tiles + T - 1) / T;                                                             \
+        if (nin)                                                                                               \
+            mma_kernel<WK, U, T, 1, true, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin); \
+        else if (xlds)                                                                                         \
+            mma_kernel<WK, U, T, 1, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+        else if (mt == 1)                                                                                      \
+            mma_kernel<WK, U, T, 1, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+        else if (mt == 2)                                                                                      \
+            mma_kernel<WK, U, T, 2, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+        else                                                                                                   \
+            mma_kernel<WK, U, T, 4, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+        TW4_LAUNCH_CHECK("mma: launch");                                                                       \
+        return TW4_OK;                                                                                         \
+    }
+    TW4_DECODE_CONFIGS(TW4_MMA_CASE)
+#undef TW4_MMA_CASE
+    tw4host::set_error("mma: unsupported warps_k / unroll / ntile %d / %d / %d", warps_k, unroll, ntile);
+    return TW4_ECONFIG;
+}
+
+}  // namespace tw4
+
 extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
                        uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, int act, void* stream) {
     int rc = check_operands("mma", x, packed, scales, zeros, y, M, N, K);
@@ -674,38 +878,49 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
     TW4_REQUIRE(M >= 1 && M <= 64, TW4_EINVAL, "mma: 1 <= M <= 64 (M = %d)", M);
     TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
                 "mma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-    TW4_REQUIRE(mt == 1 || unroll * mt <= 4, TW4_ECONFIG,
-                "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
     rc = ensure_prepared();
     if (rc) return rc;
+    return mma_launch(reinterpret_cast<const h1*>(x), reinterpret_cast<const u4*>(packed),
+                      reinterpret_cast<const h1*>(scales), reinterpret_cast<const h1*>(zeros), reinterpret_cast<h1*>(y),
+                      M, N, K, warps_k, unroll, ntile, act, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
+                               const uint16_t* norm_weight, float eps, const int32_t* packed, const uint16_t* scales,
+                               const uint16_t* zeros, uint16_t* y, int M, int N, int K, int kind, int warps_k,
+                               int unroll, int ntile, int act, void* stream) {
+    int rc = check_operands("decode_norm", x, packed, scales, zeros, y, M, N, K);
+    if (rc) return rc;
+    TW4_REQUIRE(norm_weight && reinterpret_cast<uintptr_t>(norm_weight) % 16 == 0, TW4_EINVAL,
+                "decode_norm: norm_weight must be a 16-byte aligned pointer");
+    TW4_REQUIRE(!residual || (residual_out && reinterpret_cast<uintptr_t>(residual) % 16 == 0 &&
+                              reinterpret_cast<uintptr_t>(residual_out) % 16 == 0),
+                TW4_EINVAL, "decode_norm: residual and residual_out must be 16-byte aligned pointers");
+    TW4_REQUIRE(!residual || (residual_out != residual && residual_out != x), TW4_EINVAL,
+                "decode_norm: residual_out must not alias residual or x (other workgroups still read them)");
+    TW4_REQUIRE(M >= 1 && M <= kNormMaxRows, TW4_EINVAL, "decode_norm: 1 <= M <= %d (M = %d)", kNormMaxRows, M);
+    TW4_REQUIRE(kind == 0 || kind == 1, TW4_EINVAL, "decode_norm: kind 0 (gemv) or 1 (mma), not %d", kind);
+    TW4_REQUIRE(kind == 1 || M <= 4, TW4_EINVAL, "decode_norm: gemv: 1 <= M <= 4 (M = %d)", M);
+    TW4_REQUIRE(K <= 65536, TW4_EINVAL, "decode_norm: K <= 65536 (K = %d)", K);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "decode_norm: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    rc = ensure_prepared();
+    if (rc) return rc;
+    const NormIn nin{reinterpret_cast<const h1*>(residual), reinterpret_cast<h1*>(residual_out),
+                     reinterpret_cast<const h1*>(norm_weight), eps};
     auto xp = reinterpret_cast<const h1*>(x);
     auto wp = reinterpret_cast<const u4*>(packed);
     auto sp = reinterpret_cast<const h1*>(scales);
     auto zp = reinterpret_cast<const h1*>(zeros);
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
-    const int tiles = (N + 15) >> 4;
-    const bool xlds = mt == 1 && static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
-#define TW4_MMA_CASE(WK, U, T)                                                                                \
-    if (warps_k == WK && unroll == U && ntile == T) {                                                         \
-        const size_t lds = 16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * mt * 64).total); \
-        const unsigned grid = (tiles + T - 1) / T;                                                            \
-        if (xlds)                                                                                             \
-            mma_kernel<WK, U, T, 1, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);     \
-        else if (mt == 1)                                                                                     \
-            mma_kernel<WK, U, T, 1, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
-        else if (mt == 2)                                                                                     \
-            mma_kernel<WK, U, T, 2, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
-        else                                                                                                  \
-            mma_kernel<WK, U, T, 4, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act);    \
-        TW4_LAUNCH_CHECK("mma: launch");                                                                      \
-        return TW4_OK;                                                                                        \
+    if (kind == 1) return mma_launch(xp, wp, sp, zp, yp, M, N, K, warps_k, unroll, ntile, act, &nin, st);
+    switch (M) {
+        case 1: return gemv_dispatch<1, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);
+        case 2: return gemv_dispatch<2, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);
+        case 3: return gemv_dispatch<3, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);
+        default: return gemv_dispatch<4, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);
     }
-    TW4_DECODE_CONFIGS(TW4_MMA_CASE)
-#undef TW4_MMA_CASE
-    tw4host::set_error("mma: unsupported warps_k / unroll / ntile %d / %d / %d", warps_k, unroll, ntile);
-    return TW4_ECONFIG;
 }
 
 extern "C" int tw4_decode_configs(int* out, int max_configs) {

@@ -210,6 +210,10 @@ def _table(tables: dict, device_name: str | None, device: torch.device) -> dict:
     return {}
 
 
+# Chunks (16 bytes of x) one wavefront stages in one batch: 64 lanes x 2 (kXB in tw4_decode.hip).
+FUSED_NORM_CHUNKS = 128
+
+
 class W4Linear(nn.Module):
     """Linear layer with AWQ 4-bit weights (no bias). Built with the checkpoint's AWQ tensors as
     buffers (qweight / qzeros / scales, filled by the loader, fused along the output dimension for
@@ -266,6 +270,45 @@ class W4Linear(nn.Module):
     def _gemm(self, ext, x: torch.Tensor, cfg) -> torch.Tensor:
         buf, locks = w4_hip.workspace(x.device)
         return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
+
+    def decode_entry(self, m: int) -> W4Kernel:
+        """The table entry forward uses at 1 <= M <= 16."""
+        key = (self.out_features, self.in_features, m)
+        return (self.kernels.get((*key, "silu")) if self.silu_mul else None) or self.kernels.get(key, DEFAULT_KERNEL)
+
+    def forward_norm(self, x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
+                     eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+        """self(rms_norm(x + residual) * norm_weight) and the new residual x + residual (x itself
+        without a residual): the decoder layer's add + RMSNorm before qkv_proj / gate_up_proj
+        (python/tandem/models/llama_family.py:58-65). Where the table runs the GEMV, the norm is
+        fused into the kernel's x staging (tw4_decode_norm: the same bits as the separate norm
+        kernel, one launch fewer); otherwise
+        tw4_add_rms_norm / tw4_rms_norm, then forward. x and residual are consumed (the separate
+        norm works in place). TANDEM_W4_FUSE_NORM=0 keeps the norm separate.
+
+        The fusion is used where it measured faster on MI355X (the Qwen3-8B decode step at M = 1:
+        1452 vs 1487 us): the GEMV, when each wavefront's slice of x is one staging batch (M x 16
+        chunks per quant group x its groups <= 128 chunks). A longer slice loads its later batches
+        behind the first weight chunk, whose wait then delays the next prefetch; the matrix-core
+        kernel with the fused norm (tw4_decode_norm kind 1, exact as well) measured slower than the
+        separate norm at M = 2 .. 8 (1786 vs 1691 us per step at M = 2), so the layer does not use it."""
+        from tandem_amd.layers import norm
+
+        m = x.shape[0] if x.dim() == 2 else 0
+        if (1 <= m <= 16 and not self.awq_layout and _hip_ok(x) and os.environ.get("TANDEM_W4_FUSE_NORM", "1") != "0"
+                and x.is_contiguous() and x.dtype == torch.float16):
+            kind, *cfg = self.decode_entry(m)
+            groups = self.in_features // self.group
+            one_batch = m * 16 * -(-groups // cfg[0]) <= FUSED_NORM_CHUNKS
+            if kind == "gemv" and m <= 4 and one_batch:
+                ext = w4_hip.load()
+                y, r_out = ext.w4_decode_norm(x, residual, norm_weight, eps, self.packed, self.scales, self.zeros,
+                                              0, *cfg, int(self.silu_mul))
+                return y, (r_out if residual is not None else x)
+        if residual is None:
+            return self(norm.rms_norm(x, norm_weight, eps)), x
+        xn, residual = norm.fused_add_rms_norm(x, residual, norm_weight, eps)
+        return self(xn), residual
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.awq_layout:

@@ -51,6 +51,7 @@ _SIGNATURES = {
     "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemv_f16": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_f16_configs": ([ctypes.POINTER(_I), _I], _I),
+    "tw4_decode_norm": ([_P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_rms_norm": ([_P, _P, _P, _I, _I, ctypes.c_float, _P], _I),
     "tw4_add_rms_norm": ([_P, _P, _P, _I, _I, ctypes.c_float, _P], _I),
 }
@@ -166,6 +167,26 @@ class W4Extension:
             check(self.lib.tw4_gemv_act(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
                                         int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
         return y
+
+    def w4_decode_norm(self, x, residual, norm_weight, eps: float, w, s, z, kind: int, warps_k: int, unroll: int,
+                       ntile: int, act: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """w4_gemv (kind 0) / w4_mma (kind 1) of rms_norm(x + residual) * norm_weight, the norm fused
+        into the kernel's x staging (tw4_decode_norm); returns (y, fp16(x + residual)), or (y, None)
+        without a residual. Bit-identical to tw4_add_rms_norm / tw4_rms_norm, then the kernel."""
+        m, n, k = check_operands("w4_decode_norm", x, w, s, z)
+        if residual is not None and (residual.shape != x.shape or residual.dtype != torch.float16
+                                     or not residual.is_contiguous() or residual.device != x.device):
+            raise RuntimeError("w4_decode_norm: residual must be a contiguous float16 tensor like x")
+        if norm_weight.shape != (k,) or norm_weight.dtype != torch.float16 or norm_weight.device != x.device:
+            raise RuntimeError(f"w4_decode_norm: float16 norm weight [{k}] on x's GPU expected")
+        y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
+        r_out = torch.empty_like(x) if residual is not None else None
+        with torch.cuda.device(x.device):
+            check(self.lib.tw4_decode_norm(_ptr(x), _ptr(residual) if residual is not None else None,
+                                           _ptr(r_out) if r_out is not None else None, _ptr(norm_weight), float(eps),
+                                           _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k, int(kind), int(warps_k),
+                                           int(unroll), int(ntile), int(act), _stream(x)))
+        return y, r_out
 
     def w4_mma(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int) -> torch.Tensor:
         m, n, k = check_operands("w4_mma", x, w, s, z)

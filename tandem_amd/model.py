@@ -18,7 +18,9 @@ kernel, so a captured step has the real launch sequence of a decoder layer aroun
 
 Projections are W4Linear (AutoAWQ checkpoints) or nn.Linear (fp16 checkpoints); ``prepare`` moves
 the model to the GPU, repacks the W4 layers and routes the fp16 projections and the logits head
-through layers/gemv16.py's table. Norms run on tw4_rms_norm / tw4_add_rms_norm.
+through layers/gemv16.py's table. Norms run on tw4_rms_norm / tw4_add_rms_norm, or inside the W4
+qkv_proj / gate_up_proj kernels where W4Linear.forward_norm can fuse them (the decode GEMV and the
+matrix-core decode kernel: a norm kernel fewer before each, the same bits).
 """
 
 from __future__ import annotations
@@ -123,14 +125,22 @@ class DecoderLayer(nn.Module):
         """The residual stream is carried between layers, so every "add residual, then normalise"
         pair is one kernel (python/tandem/models/llama_family.py:47-67)."""
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
-        if residual is None:
-            residual = hidden
-            hidden = norm.rms_norm(hidden, n1.weight, n1.eps)
+        attn, mlp = self.self_attn, self.mlp
+        if hasattr(attn.qkv_proj, "forward_norm"):  # W4: the norm goes into the projection's prologue
+            qkv, residual = attn.qkv_proj.forward_norm(hidden, residual, n1.weight, n1.eps)
+            hidden = attn.o_proj(attn.attend(qkv))
         else:
-            hidden, residual = norm.fused_add_rms_norm(hidden, residual, n1.weight, n1.eps)
-        hidden = self.self_attn(hidden)
+            if residual is None:
+                residual = hidden
+                hidden = norm.rms_norm(hidden, n1.weight, n1.eps)
+            else:
+                hidden, residual = norm.fused_add_rms_norm(hidden, residual, n1.weight, n1.eps)
+            hidden = attn(hidden)
+        if hasattr(mlp.gate_up_proj, "forward_norm"):
+            act, residual = mlp.gate_up_proj.forward_norm(hidden, residual, n2.weight, n2.eps)
+            return mlp.down_proj(act if mlp.fused_act else silu_and_mul(act)), residual
         hidden, residual = norm.fused_add_rms_norm(hidden, residual, n2.weight, n2.eps)
-        return self.mlp(hidden), residual
+        return mlp(hidden), residual
 
 
 class DecoderModel(nn.Module):

@@ -128,6 +128,62 @@ def test_gemv_silu_mul(ext):
                 check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
 
 
+def _norm_inputs(m: int, k: int, seed: int):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((m, k)) * 2).astype(np.float16)
+    r = (rng.standard_normal((m, k)) * 8).astype(np.float16)
+    w = (rng.random(k) + 0.5).astype(np.float16)
+    return x, r, w
+
+
+@pytest.mark.parametrize("kind", ["gemv", "mma"])
+def test_decode_norm_matches_separate_norm(ext, kind):
+    """The fused norm prologue (tw4_decode_norm) equals tw4_add_rms_norm / tw4_rms_norm followed by
+    the same kernel and config, bit for bit, and so does its residual output; every config, with
+    and without the SwiGLU epilogue, with and without a residual."""
+    from tandem_amd.layers import norm
+
+    k01 = 0 if kind == "gemv" else 1
+    run = (lambda xx, c, cfg, act: ext.w4_gemv(xx, c.packed, c.s, c.zz, *cfg, act)) if kind == "gemv" else \
+        (lambda xx, c, cfg, act: ext.w4_mma(xx, c.packed, c.s, c.zz, *cfg, act))
+    for k, n, act in ((512, 64, 0), (1024, 512, 1), (2048, 520, 0), (4096, 1024, 1)):
+        c = Case(k, n, seed=21, interleave=bool(act))
+        for m in ((1, 2, 3, 4) if kind == "gemv" else (1, 3, 8, 9, 16)):
+            if kind == "mma" and m * (k // 8 + 1) * 16 > 80 * 1024:
+                with pytest.raises(RuntimeError, match="fused norm"):
+                    ext.w4_decode_norm(gpu(np.zeros((m, k), np.float16)), None, gpu(np.ones(k, np.float16)), 1e-6,
+                                       c.packed, c.s, c.zz, 1, *DECODE_CONFIGS[0], act)
+                continue
+            x, r, w = _norm_inputs(m, k, seed=900 + m)
+            xg, rg, wg = gpu(x), gpu(r), gpu(w)
+            xs, rs = xg.clone(), rg.clone()
+            norm.fused_add_rms_norm(xs, rs, wg, 1e-6)
+            xp = norm.rms_norm(xg, wg, 1e-6)
+            for cfg in DECODE_CONFIGS:
+                y, r_out = ext.w4_decode_norm(xg, rg, wg, 1e-6, c.packed, c.s, c.zz, k01, *cfg, act)
+                assert torch.equal(r_out, rs), (k, n, m, cfg)
+                assert torch.equal(y, run(xs, c, cfg, act)), (k, n, m, cfg, act)
+                y2, none = ext.w4_decode_norm(xg, None, wg, 1e-6, c.packed, c.s, c.zz, k01, *cfg, act)
+                assert none is None and torch.equal(y2, run(xp, c, cfg, act)), (k, n, m, cfg, act)
+            assert torch.equal(xg, gpu(x)) and torch.equal(rg, gpu(r))  # inputs untouched
+
+
+def test_decode_norm_small_k_against_oracle(ext):
+    """K = 128 and 384 (one or three quant groups: some wavefronts have no slice and only join the
+    workgroup barrier) against the oracle's norm and product, GEMV / matrix-core tolerances."""
+    for k, n in ((128, 32), (384, 48)):
+        c = Case(k, n, seed=22)
+        for m in (1, 4):
+            x, r, w = _norm_inputs(m, k, seed=950 + m)
+            a, r2 = o.add_rms_norm(x, r, w, 1e-6)
+            ref = o.linear(a, c.w_exact)
+            for cfg in DECODE_CONFIGS:
+                for k01, atol, rtol in ((0, 0.05, 0.02), (1, 0.02, 0.01)):
+                    y, r_out = ext.w4_decode_norm(gpu(x), gpu(r), gpu(w), 1e-6, c.packed, c.s, c.zz, k01, *cfg, 0)
+                    assert (r_out.cpu().numpy().view(np.uint16) == r2.view(np.uint16)).all()
+                    check_close(y, ref, atol, rtol, (k, n, m, cfg, k01))
+
+
 def test_mma_every_config(ext):
     """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229)."""
     for k, n in SHAPES:

@@ -184,6 +184,33 @@ def test_tiny_decoder_step_matches_oracle():
 
 
 @pytest.mark.gpu
+def test_fused_norm_step_is_bit_identical(monkeypatch):
+    """The step with the norms fused into qkv_proj / gate_up_proj (the default) and with separate
+    norm kernels (TANDEM_W4_FUSE_NORM=0) gives the same logits, bit for bit."""
+    model, _ = _tiny_model(seed=3)
+    for mod in model.modules():  # GEMV entries for M <= 4, where the layer fuses the norm
+        if hasattr(mod, "forward_norm"):
+            for m in range(1, 5):
+                mod.kernels[(mod.out_features, mod.in_features, m)] = ("gemv", 4, 1, 1)
+                mod.kernels[(mod.out_features, mod.in_features, m, "silu")] = ("gemv", 8, 1, 1)  # empty slices
+    from tandem_amd.layers import w4_hip
+
+    calls = []
+    real = w4_hip.W4Extension.w4_decode_norm
+    monkeypatch.setattr(w4_hip.W4Extension, "w4_decode_norm", lambda self, *a: calls.append(1) or real(self, *a))
+    for ids in ([5], [1, 2, 3], [4, 4, 9, 1], list(range(10, 26))):
+        t = torch.tensor(ids, device="cuda")
+        calls.clear()
+        with torch.inference_mode():
+            fused = model.compute_logits(model(t))
+            assert len(calls) == (2 * TINY.num_layers if len(ids) <= 4 else 0), (ids, len(calls))
+            monkeypatch.setenv("TANDEM_W4_FUSE_NORM", "0")
+            separate = model.compute_logits(model(t))
+            monkeypatch.delenv("TANDEM_W4_FUSE_NORM")
+        assert torch.equal(fused, separate), ids
+
+
+@pytest.mark.gpu
 def test_graph_runner_matches_eager_buckets():
     """Each bucket's replay equals the eager step on the same padded batch, bit for bit, and stays
     so over repeated replays with eager work and synchronisations in between."""

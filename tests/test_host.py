@@ -250,3 +250,45 @@ def test_bench_refuses_more_than_one_gpu():
     proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                           text=True, timeout=300)
     assert proc.returncode != 0 and "one GPU" in proc.stderr
+
+
+# -------------------------------------------------------------- staging index math (host check)
+def _x_slice(gb, ge, m):
+    """x_slice of csrc/tw4_decode.hip: (c0, n16, n, magic)."""
+    n16 = 16 * (ge - gb)
+    return (16 * gb if n16 else 0), n16, m * n16, ((0xFFFFFFFF // n16) + 1 if n16 else 0)
+
+
+def _x_pos(sl, f, one_row):
+    c0, n16, n, magic = sl
+    f = max(min(f, n - 1), 0)
+    if one_row:
+        return 0, f
+    mm = (f * magic) >> 32
+    return mm, f - mm * n16
+
+
+@pytest.mark.parametrize("k", [128, 256, 384, 512, 1024, 4096, 12288])
+def test_staging_indices_in_bounds(k):
+    """Every chunk the decode kernels' x staging and the fused norm prologue load (the first batch
+    and every later batch, including the unconditional loads of an empty slice) lies inside x [M, K],
+    the norm weight [K] and the [M][G] group-sum table, and the umulhi division is exact; for every
+    compiled warps_k and M = 1..16."""
+    kx, g_count = k // 8, k // 128
+    for wk in sorted({c[0] for c in w4_hip.decode_configs()}):
+        gw = -(-g_count // wk)
+        for m in range(1, 17):
+            for wave in range(wk):
+                gb = min(wave * gw, g_count)
+                ge = min(gb + gw, g_count)
+                sl = _x_slice(gb, ge, m)
+                c0, n16, n, _ = sl
+                last = max(n, 128) + 64 * 2  # the first batch always, then batches while f0 - lane < n
+                for lane in range(64):
+                    for f in range(lane, last, 64):
+                        mm, c = _x_pos(sl, f, m == 1)
+                        assert 0 <= mm < m and 0 <= c0 + c < kx, (k, wk, m, wave, f)
+                        assert mm * kx + c0 + c < m * kx
+                        if n and f < n:  # the exact position of a real chunk
+                            assert (mm, c) == divmod(f, n16)
+                            assert mm * g_count + (c0 + c) // 16 < m * g_count
