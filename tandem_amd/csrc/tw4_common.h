@@ -100,6 +100,16 @@ __device__ __forceinline__ u4 load_stream(const u4* p) {  // weights: read once,
     return __builtin_nontemporal_load(p);
 }
 
+// Raw buffer resource word 3 for gfx9-family data loads (32-bit data format, no swizzle).
+constexpr int kBufferFlags = 0x00020000;
+
+// Lane `lane`'s 16 bytes of weight block g of a tile, through the tile's buffer resource: the
+// block offset g * 1024 goes in the scalar offset and the lane offset in the vector one, so a
+// stream of blocks costs no per-lane 64-bit address arithmetic. Non-temporal (aux = 2: nt).
+__device__ __forceinline__ u4 load_block(__amdgpu_buffer_rsrc_t rs, int g, int lane) {
+    return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, g * (kBlockU4 * 16), 2));
+}
+
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
 // Cross-lane exchanges on the VALU (DPP and gfx950's permlane swaps) instead of the LDS crossbar.

@@ -52,12 +52,21 @@ __device__ __forceinline__ void scale_zero(uint32_t p, uint32_t& s, uint32_t& z)
     z = sz[1];
 }
 
+// Workgroups are dealt to the 8 XCDs round robin (workgroup b runs on XCD b mod 8). Within each full
+// group of 8 workgroups the tile index is rotated by b / 8, so the tiles one XCD streams do not all
+// share the same low address bits: measured on MI355X, the XCDs then finish closer together (the
+// M = 1 GEMV on gate_up 10.3 vs 10.4-10.6 us). A permutation of 0 .. gridDim.x - 1.
+__device__ __forceinline__ int xcd_rotated_block() {
+    const int b = blockIdx.x, full = gridDim.x & ~7;
+    return b < full ? (b & ~7) | (((b & 7) + (b >> 3)) & 7) : b;
+}
+
 // The workgroup's row tiles. Everything but `lane` and `prow` is uniform across the wavefront (the
 // tile index comes from blockIdx), so tile and group offsets stay in scalar registers and each
 // load is one scalar base + the lane's fixed vector offset.
 template <int NT>
 struct TileStreams {
-    const u4* w[NT];     // group 0 block of the tile
+    __amdgpu_buffer_rsrc_t w[NT];  // the tile's weight blocks (G KB): block g at byte g * 1024
     int64_t p[NT];       // scale / zero offset of (tile, group 0) in the tile-major order
     int rows[NT];        // rows of the tile: the scale / zero stride between groups
     int prow[NT];        // this lane's row in the tile (clamped: padding rows have zero weights)
@@ -75,7 +84,8 @@ __device__ __forceinline__ TileStreams<NT> tile_streams(const u4* w, const uint1
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int tt = min(tile0 + t, tiles - 1);  // tiles past the end recompute the last one; not stored
-        ts.w[t] = w + static_cast<int64_t>(tt) * G * kBlockU4;
+        ts.w[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<u4*>(w + static_cast<int64_t>(tt) * G * kBlockU4), 0,
+                                                    G * kBlockU4 * 16, kBufferFlags);
         ts.rows[t] = tile_rows(tt, N);
         ts.p[t] = static_cast<int64_t>(16) * tt * G;
         ts.prow[t] = min(r, ts.rows[t] - 1);
@@ -124,7 +134,7 @@ __device__ __forceinline__ void load_chunk(WeightSet<U, NT>& ws, const TileStrea
         const int g = min(g0 + u, glast);  // past the range: a valid block, given scale 0 below
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            ws.w[u][t] = load_stream(ts.w[t] + static_cast<int64_t>(g) * kBlockU4 + ts.lane);
+            ws.w[u][t] = load_block(ts.w[t], g, ts.lane);
             const int64_t pg = ts.p[t] + static_cast<int64_t>(g) * ts.rows[t];
             ws.p[u][t] = (ts.pb + pg)[ts.prow[t]];
         }
@@ -182,7 +192,7 @@ __device__ __forceinline__ void load_x_batch(u4 (&v)[kXB], const u4* xg, int kx,
 
 // Flat chunk f into LDS. BIASED: as x' (pairs k = 8 j + 2, 3 and 8 j + 6, 7 divided by 16: exact, a
 // power-of-two scale, rounded only where x / 16 is below fp16's normal range) plus, per (m, group,
-// 32-k slice kb), the float sums A = sum x' and B = sum x of the slice (corr[(m G + g) 4 + kb],
+// 32-k slice kb), the float sums -1024 A (A = sum x') and B = sum x of the slice (corr[(m G + g) 4 + kb],
 // float2). A word's four magic halves (1024 + q for weights 8 j + 0, 1 and 8 j + 4, 5; 1024 + 16 q
 // for 8 j + 2, 3 and 8 j + 6, 7) dotted with x' give sum q x + 1024 sum x', so
 // sum (q - z) x = dot - 1024 A - z B. The four chunks of a 32-k slice are lanes 4 i .. 4 i + 3 of
@@ -213,7 +223,7 @@ __device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, floa
         b += lane_xor2(b);
         smem[p.m * l.xs + col] =
             u4{bitcast<uint32_t>(y0), bitcast<uint32_t>(y1), bitcast<uint32_t>(y2), bitcast<uint32_t>(y3)};
-        if ((col & 3) == 0 && f < xs.n) corr[p.m * (kx >> 2) + (col >> 2)] = float2{a, b};
+        if ((col & 3) == 0 && f < xs.n) corr[p.m * (kx >> 2) + (col >> 2)] = float2{-1024.0f * a, b};
     }
 }
 
@@ -388,11 +398,15 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
         const int graw = g0 + u;
         const bool valid = graw < ge;
         const int g = min(graw, ge - 1);
+        // the slice's sums start at -1024 A (the bias correction, precomputed) and take the dots
         float part[NT][M];
+        float2 c[M];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int m = 0; m < M; ++m) {
+            c[m] = corr[(m * G + g) * 4 + kb];
 #pragma unroll
-            for (int m = 0; m < M; ++m) part[t][m] = 0.0f;
+            for (int t = 0; t < NT; ++t) part[t][m] = c[m].x;
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             u4 xq[M];  // x'[m][128 g + 32 kb + 8 s .. + 7]
@@ -412,16 +426,15 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
             }
         }
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float2 c = corr[(m * G + g) * 4 + kb];
+        for (int t = 0; t < NT; ++t) {
+            uint32_t s_raw, z_raw;
+            scale_zero(cur.p[u][t], s_raw, z_raw);
+            const float sc = static_cast<float>(as_h1(s_raw));
+            const float zf = static_cast<float>(as_h1(z_raw));
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                uint32_t s_raw, z_raw;
-                scale_zero(cur.p[u][t], s_raw, z_raw);
-                const float sc = valid ? static_cast<float>(as_h1(s_raw)) : 0.0f;
-                const float zf = static_cast<float>(as_h1(z_raw));
-                const float v = __builtin_fmaf(-zf, c.y, __builtin_fmaf(-1024.0f, c.x, part[t][m]));
-                acc[t][m] = __builtin_fmaf(v, sc, acc[t][m]);
+            for (int m = 0; m < M; ++m) {
+                const float v = __builtin_fmaf(-zf, c[m].y, part[t][m]);
+                acc[t][m] = valid ? __builtin_fmaf(v, sc, acc[t][m]) : acc[t][m];
             }
         }
     }
@@ -435,7 +448,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int tile0 = blockIdx.x * NT;
+    const int tile0 = xcd_rotated_block() * NT;
     const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, NT), NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
