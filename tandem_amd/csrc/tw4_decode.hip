@@ -395,9 +395,10 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math: the scheduler would sink it
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+        // a chunk that prefetches is not the wavefront's last: all its groups are in range
         const int graw = g0 + u;
-        const bool valid = graw < ge;
-        const int g = min(graw, ge - 1);
+        const bool valid = PF || graw < ge;
+        const int g = PF ? graw : min(graw, ge - 1);
         // the slice's sums start at -1024 A (the bias correction, precomputed) and take the dots
         float part[NT][M];
         float2 c[M];
@@ -570,9 +571,9 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
     __builtin_amdgcn_sched_barrier(0);  // keep the loads above the math: the scheduler would sink them
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int graw = g0 + u;
-        const bool valid = graw < ge;
-        const int g = min(graw, ge - 1);
+        const int graw = g0 + u;  // a chunk that prefetches is not the last: all its groups are in range
+        const bool valid = PF || graw < ge;
+        const int g = PF ? graw : min(graw, ge - 1);
         GroupQ p[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -613,7 +614,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int tile0 = blockIdx.x * NT;
+    const int tile0 = xcd_rotated_block() * NT;
     const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * MT * 64, NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
