@@ -113,7 +113,7 @@ def kernel_of(awq, lin, m: int) -> str:
     if m <= 16:
         key = (lin.out_features, lin.in_features, m)
         kind = (lin.kernels.get((*key, "silu")) if lin.silu_mul else None) or lin.kernels.get(key, awq.DEFAULT_KERNEL)
-        if kind[0] == "gemv" and m > 4:
+        if kind[0] in ("gemv", "gemvm") and m > 4:
             kind = awq.DEFAULT_KERNEL
         return f"{kind[0]}{tuple(kind[1:])}"
     key = (lin.out_features, lin.in_features) + (("silu",) if lin.silu_mul else ())

@@ -96,6 +96,15 @@ int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scale
                  const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                  int warps_k, int unroll, int ntile, int act, void* stream);
 
+/* The GEMV's arithmetic on the matrix cores, 1 <= M <= 4: raw magic halves (1024 + q) times x' on
+ * v_mfma_f32_16x16x32_f16, the bias and the zero point in the accumulator's start value, the scale
+ * per group; exact (q - z) weights like tw4_gemv (so the GEMV's tolerance). Same configs, act and
+ * limits as tw4_gemv_act (scales and zeros 8-byte aligned). No reference counterpart: an alternative
+ * kernel for the (N, K, M) table entries of w4_gemv (python/tandem/layers/awq.py:136-160). */
+int tw4_gemv_mfma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+                  const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+                  int warps_k, int unroll, int ntile, int act, void* stream);
+
 /* The decoder layer's add + RMSNorm fused into a decode kernel's x staging: the kernel
  * (kind 0: tw4_gemv_act, 1 <= M <= 4; kind 1: tw4_mma with x in LDS, 1 <= M <= 16 and
  * M (K + 8) 2 <= 80 KB) runs on a = fp16((x + residual) * rsqrt(mean((x + residual)^2) + eps)

@@ -547,6 +547,188 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     }
 }
 
+// ----------------------------------------------------------------------------------- gemvm
+// The GEMV's arithmetic on the matrix cores, M <= 4. A = the raw magic halves of a word (1024 + q,
+// or 1024 + 16 q for the high nibbles: no zero point, no scale), B = x' (pairs 2, 3, 6, 7 divided
+// by 16), so one v_mfma_f32_16x16x32_f16 does the 32 products that take 16 v_dot2 per batch row
+// on the vector ALUs. The bias and the zero point come off in the accumulator's start value,
+// D0 = -1024 A_g - z B_g (A_g / B_g: the group's sums of x' / x), and the group's scale after its
+// four MFMAs: acc += s (D0 + sum (1024 + q) x'). The weights are exact (q - z) as in the GEMV
+// (not the fp16-rounded (q - z) s of the mma kernel), so this is a GEMV-class kernel for tolerance
+// purposes. Lane (kb, r) holds D rows 4 kb + i of batch column r: it loads the scales and zeros of
+// rows 4 kb .. 4 kb + 3 with two 8-byte loads per group.
+template <int U, int NT>
+struct WeightSetM {
+    u4 w[U][NT];
+    u2 s[U][NT];  // fp16 scales of rows 4 kb .. 4 kb + 3
+    u2 z[U][NT];  // fp16 zeros of the same rows
+};
+
+template <int U, int NT>
+__device__ __forceinline__ void load_chunk_m(WeightSetM<U, NT>& ws, const TileStreams<NT>& ts, const uint16_t* s16,
+                                             const uint16_t* z16, int g0, int glast, int kb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = min(g0 + u, glast);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            ws.w[u][t] = load_block(ts.w[t], g, ts.lane);
+            // rows 4 kb .. 4 kb + 3 of the tile; a short last tile (8 rows) reads rows 4 .. 7 for kb >= 2
+            const int row0 = min(4 * kb, ts.rows[t] - 4);
+            const int64_t off = ts.p[t] + static_cast<int64_t>(g) * ts.rows[t] + row0;
+            ws.s[u][t] = *reinterpret_cast<const u2*>(s16 + off);
+            ws.z[u][t] = *reinterpret_cast<const u2*>(z16 + off);
+        }
+    }
+}
+
+__host__ __device__ __forceinline__ int gemvm_gcorr_u4(int M, int K) { return (M * (K >> 7) * 8 + 15) / 16; }
+
+// After staging: the group sums (-1024 A_g, B_g) of the wavefront's groups from the slice sums.
+template <int M>
+__device__ __forceinline__ void group_corr(const float2* corr, float2* gcorr, int G, int gb, int ge, int lane) {
+    const int n = (ge - gb) * M;
+    for (int j = lane; j < n; j += 64) {
+        const int m = j / (ge - gb), g = gb + (j - m * (ge - gb));
+        const float2* c = corr + (m * G + g) * 4;
+        gcorr[m * G + g] = float2{(c[0].x + c[1].x) + (c[2].x + c[3].x), (c[0].y + c[1].y) + (c[2].y + c[3].y)};
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool PF, int M, int U, int NT>
+__device__ __forceinline__ void gemvm_chunk(const WeightSetM<U, NT>& cur, WeightSetM<U, NT>& nxt,
+                                            const TileStreams<NT>& ts, const uint16_t* s16, const uint16_t* z16,
+                                            const u4* lx, const float2* gcorr, const DecodeLds& l, f4 (&acc)[NT],
+                                            int xrow, int g0, int ge, int G, int kb, uint32_t magic) {
+    if constexpr (PF) load_chunk_m<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1, kb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int graw = g0 + u;  // a chunk that prefetches is not the last: all its groups are in range
+        const bool valid = PF || graw < ge;
+        const int g = PF ? graw : min(graw, ge - 1);
+        const float2 gc = gcorr[xrow * G + g];
+        h8 xb[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xb[s] = bitcast<h8>(lx[xrow * l.xs + 16 * g + 4 * kb + s]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const h4 z4 = bitcast<h4>(cur.z[u][t]);
+            f4 d;
+            d.x = __builtin_fmaf(-static_cast<float>(z4.x), gc.y, gc.x);
+            d.y = __builtin_fmaf(-static_cast<float>(z4.y), gc.y, gc.x);
+            d.z = __builtin_fmaf(-static_cast<float>(z4.z), gc.y, gc.x);
+            d.w = __builtin_fmaf(-static_cast<float>(z4.w), gc.y, gc.x);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                h2 q[4];
+                unpack_raw(word_of(cur.w[u][t], s), magic, q);
+                const h8 a = h8{q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
+                d = mfma16x16x32(a, xb[s], d);
+            }
+            if (valid) {
+                const h4 s4 = bitcast<h4>(cur.s[u][t]);
+                acc[t].x = __builtin_fmaf(static_cast<float>(s4.x), d.x, acc[t].x);
+                acc[t].y = __builtin_fmaf(static_cast<float>(s4.y), d.y, acc[t].y);
+                acc[t].z = __builtin_fmaf(static_cast<float>(s4.z), d.z, acc[t].z);
+                acc[t].w = __builtin_fmaf(static_cast<float>(s4.w), d.w, acc[t].w);
+            }
+        }
+    }
+}
+
+template <int M, int WK, int U, int NT>
+__global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
+                                                       const h1* __restrict__ scales, const h1* __restrict__ zeros,
+                                                       h1* __restrict__ y, int N, int K, int act) {
+    extern __shared__ u4 smem[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
+    const int r = lane & 15, kb = lane >> 4;
+    const int G = K >> 7, tiles = (N + 15) >> 4;
+    const int tile0 = xcd_rotated_block() * NT;
+    const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K) + gemvm_gcorr_u4(M, K), (WK - 1) * NT * 64);
+    const uint32_t magic = magic_reg();
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
+    const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
+    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
+    const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
+    const int nch = (ge - gb + U - 1) / U;
+    float2* corr = reinterpret_cast<float2*>(smem + l.corr);
+    float2* gcorr = reinterpret_cast<float2*>(smem + l.corr + gemv_corr_u4(M, K));
+    const int xrow = min(r, M - 1);  // B columns past M: any valid row, their D columns are not stored
+
+    const int kx = K >> 3;
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    const XSlice xsl = x_slice(gb, ge, M);
+    WeightSetM<U, NT> a, b;
+    if (nch > 0) {
+        u4 xfirst[kXB];
+        load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk_m<U, NT>(a, ts, s16, z16, gb, ge - 1, kb);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_x<true, M == 1>(smem, l, corr, xg, kx, xsl, xfirst, lane);
+        group_corr<M>(corr, gcorr, G, gb, ge, lane);
+    }
+
+    f4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int i = 0;
+    for (; i + 2 < nch; i += 2) {
+        gemvm_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+        gemvm_chunk<true, M, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
+    }
+    if (i + 2 == nch) {
+        gemvm_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+        gemvm_chunk<false, M, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
+    } else if (i + 1 == nch) {
+        gemvm_chunk<false, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+    }
+    if (WK > 1) {
+        f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][64]
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) red[((wave - 1) * NT + t) * 64 + lane] = acc[t];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int v = 0; v < WK - 1; ++v)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] += red[(v * NT + t) * 64 + lane];
+    }
+    if (act) {  // N % 16 == 0: gate rows 4 kb + i (kb = 0, 1) in lane l, up rows 8 + 4 kb + i in lane l + 32
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = tile0 + t;
+            f4 up;
+            up.x = lane_xor32(acc[t].x, lane);
+            up.y = lane_xor32(acc[t].y, lane);
+            up.z = lane_xor32(acc[t].z, lane);
+            up.w = lane_xor32(acc[t].w, lane);
+            if (kb >= 2 || r >= M || tt >= tiles) continue;
+            const f4 g4 = acc[t];
+            *reinterpret_cast<h4*>(y + static_cast<int64_t>(r) * half_n + 8 * tt + 4 * kb) =
+                h4{static_cast<h1>(silu(g4.x) * up.x), static_cast<h1>(silu(g4.y) * up.y),
+                   static_cast<h1>(silu(g4.z) * up.z), static_cast<h1>(silu(g4.w) * up.w)};
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = 16 * (tile0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+        if (n >= N || r >= M) continue;
+        const f4 a4 = acc[t];
+        *reinterpret_cast<h4*>(y + static_cast<int64_t>(r) * N + n) =
+            h4{static_cast<h1>(a4.x), static_cast<h1>(a4.y), static_cast<h1>(a4.z), static_cast<h1>(a4.w)};
+    }
+}
+
 // ------------------------------------------------------------------------------------- mma
 // MT batch tiles of 16 columns (M <= 16 MT): lane (kb, r) feeds B column r of tile b = token
 // 16 b + r, and D tile (t, b) holds rows 4 kb + i of that token. Each dequantized A fragment feeds
@@ -758,6 +940,10 @@ int decode_prepare(int dev) {
 #define TW4_ATTR(WK, U, T)                                                   \
     TW4_ATTR_GEMV(WK, U, T, false)                                           \
     TW4_ATTR_GEMV(WK, U, T, true)                                            \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<1, WK, U, T>);             \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<2, WK, U, T>);             \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<3, WK, U, T>);             \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<4, WK, U, T>);             \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true>);         \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true, true>);   \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, false>);        \
@@ -795,6 +981,26 @@ int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int
     TW4_DECODE_CONFIGS(TW4_GEMV_CASE)
 #undef TW4_GEMV_CASE
     tw4host::set_error("gemv: unsupported warps_k / unroll / ntile %d / %d / %d", wk, un, nt);
+    return TW4_ECONFIG;
+}
+
+template <int M>
+int gemvm_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
+                   int act, hipStream_t st) {
+    const int tiles = (N + 15) >> 4;
+#define TW4_GEMVM_CASE(WK, U, T)                                                                             \
+    if (wk == WK && un == U && nt == T) {                                                                    \
+        const size_t lds = 16 * static_cast<size_t>(                                                         \
+                                    decode_lds(true, M, K, gemv_corr_u4(M, K) + gemvm_gcorr_u4(M, K), (WK - 1) * T * 64).total); \
+        TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
+                    "gemv_mfma: x [%d, %d] does not fit in LDS (use mma)", M, K);                            \
+        gemvm_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act);       \
+        TW4_LAUNCH_CHECK("gemv_mfma: launch");                                                               \
+        return TW4_OK;                                                                                       \
+    }
+    TW4_DECODE_CONFIGS(TW4_GEMVM_CASE)
+#undef TW4_GEMVM_CASE
+    tw4host::set_error("gemv_mfma: unsupported warps_k / unroll / ntile %d / %d / %d", wk, un, nt);
     return TW4_ECONFIG;
 }
 
@@ -838,6 +1044,33 @@ extern "C" int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint
         case 2: return gemv_dispatch<2, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
         case 3: return gemv_dispatch<3, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
         default: return gemv_dispatch<4, false>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, none, st);
+    }
+}
+
+extern "C" int tw4_gemv_mfma(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                             uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, int act,
+                             void* stream) {
+    int rc = check_operands("gemv_mfma", x, packed, scales, zeros, y, M, N, K);
+    if (rc) return rc;
+    TW4_REQUIRE(M >= 1 && M <= 4, TW4_EINVAL, "gemv_mfma: 1 <= M <= 4 (M = %d; larger M: mma)", M);
+    TW4_REQUIRE(reinterpret_cast<uintptr_t>(scales) % 8 == 0 && reinterpret_cast<uintptr_t>(zeros) % 8 == 0,
+                TW4_EINVAL, "gemv_mfma: scales and zeros must be 8-byte aligned");
+    TW4_REQUIRE(K <= 65536, TW4_EINVAL, "gemv_mfma: K <= 65536 (K = %d; larger K: mma)", K);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "gemv_mfma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    rc = ensure_prepared();
+    if (rc) return rc;
+    auto xp = reinterpret_cast<const h1*>(x);
+    auto wp = reinterpret_cast<const u4*>(packed);
+    auto sp = reinterpret_cast<const h1*>(scales);
+    auto zp = reinterpret_cast<const h1*>(zeros);
+    auto yp = reinterpret_cast<h1*>(y);
+    auto st = static_cast<hipStream_t>(stream);
+    switch (M) {
+        case 1: return gemvm_dispatch<1>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        case 2: return gemvm_dispatch<2>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        case 3: return gemvm_dispatch<3>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
+        default: return gemvm_dispatch<4>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
     }
 }
 

@@ -139,6 +139,8 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 # `python -m tandem_amd.tune` sweeps on the GPU:
 #   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4 (with the SwiGLU epilogue too: the
 #                                      reference's SwiGLU gate_up always takes "mma")
+#   ("gemvm", warps_k, unroll, ntile)  the GEMV's arithmetic (exact q - z, scale per group) on the
+#                                      matrix cores, M <= 4
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
 #   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
@@ -327,7 +329,9 @@ class W4Linear(nn.Module):
                     return self._gemm(ext, x, cfg)
                 if kind == "gemv" and m <= 4:  # with the SwiGLU epilogue too (tw4_gemv_act)
                     return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
-                if kind != "mma":  # gemv past M = 4
+                if kind == "gemvm" and m <= 4:  # the GEMV's arithmetic on the matrix cores
+                    return ext.w4_gemv_mfma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
+                if kind != "mma":  # gemv / gemvm past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
         elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul

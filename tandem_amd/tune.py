@@ -146,6 +146,13 @@ def main(argv=None) -> int:
                     except RuntimeError:
                         continue
                     res[("gemv", *cfg)] = us
+            if "gemvm" in kinds and m <= 4:
+                for cfg in w4_hip.decode_configs():
+                    try:
+                        us = time_us([lambda w=w, c=cfg: ext.w4_gemv_mfma(x, *w, *c, act) for w in ws], stream)
+                    except RuntimeError:
+                        continue
+                    res[("gemvm", *cfg)] = us
             if "mma" in kinds and m <= 64:
                 for cfg in w4_hip.decode_configs():
                     try:

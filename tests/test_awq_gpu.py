@@ -128,6 +128,29 @@ def test_gemv_silu_mul(ext):
                 check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
 
 
+def test_gemv_mfma_every_config(ext):
+    """The GEMV's arithmetic on the matrix cores (tw4_gemv_mfma), M = 1..4, every compiled config,
+    plain and SwiGLU, at the GEMV's tolerance (exact q - z weights, like w4_gemv)."""
+    for k, n in SHAPES:
+        c = Case(k, n, seed=31)
+        for m in range(1, 5):
+            x = c.x(m, seed=1100 + m)
+            ref = o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                check_close(ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg))
+    for k, n in ((128, 32), (1024, 512), (4096, 1024)):
+        c = Case(k, n, seed=32, interleave=True)
+        for m in range(1, 5):
+            x = c.x(m, seed=1200 + m)
+            ref = o.swiglu_reference(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                y = ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg, 1)
+                assert y.shape == (m, n // 2)
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
+
+
 def _norm_inputs(m: int, k: int, seed: int):
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((m, k)) * 2).astype(np.float16)

@@ -212,8 +212,8 @@ def test_tables_are_well_formed():
             assert 1 <= m <= 16 and k % 128 == 0 and n % 8 == 0
             if cfg[0] == "gemm":  # a compiled GEMM config and a split mode
                 assert len(cfg) == 7 and tuple(cfg[1:6]) in gemm and 0 <= cfg[6] <= 16
-            else:  # a compiled decode config; gemv only where it runs (M <= 4)
-                assert cfg[0] in ("gemv", "mma") and tuple(cfg[1:]) in decode
+            else:  # a compiled decode config; gemv / gemvm only where they run (M <= 4)
+                assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
                 assert cfg[0] == "mma" or m <= 4
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
         m_maxes = [m for m, _ in ladder]
