@@ -59,6 +59,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-detail", action="store_true", help="skip the per-projection sweep")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the decode_step section (for profiling the whole step); prints its JSON")
     return ap.parse_args()
 
 
@@ -218,6 +220,9 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     w4_hip.load()
+    if a.step_only:
+        print(json.dumps({"decode_step": decode_step(torch, dev)}), flush=True)
+        return 0
     m = a.m
     layers = make_layers(torch, awq, a.layers, dev)
     stream = torch.cuda.Stream(dev)
