@@ -264,13 +264,16 @@ struct NormIn {
 
 constexpr int kNormMaxRows = 16;
 
-__device__ __forceinline__ void norm_sum(const u4& xv, const u4& rv, bool has_r, float (&s)[8]) {
-    chunk_to_f32(xv, s);
-    if (has_r) {
-        float b[8];
-        chunk_to_f32(rv, b);
+// s = x + r per element, as one fma on the fp16 operands (v_fma_mix_f32: no conversions): r * rw + x
+// with rw = 1 (a residual) or 0 (none: rv then holds x, and x + x * 0 = x). The same bits as
+// converting both and adding in fp32.
+__device__ __forceinline__ void norm_sum(const u4& xv, const u4& rv, float rw, float (&s)[8]) {
+    const h2 x[4] = {bitcast<h2>(xv.x), bitcast<h2>(xv.y), bitcast<h2>(xv.z), bitcast<h2>(xv.w)};
+    const h2 r[4] = {bitcast<h2>(rv.x), bitcast<h2>(rv.y), bitcast<h2>(rv.z), bitcast<h2>(rv.w)};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] += b[i];
+    for (int i = 0; i < 4; ++i) {
+        s[2 * i] = __builtin_fmaf(static_cast<float>(r[i].x), rw, static_cast<float>(x[i].x));
+        s[2 * i + 1] = __builtin_fmaf(static_cast<float>(r[i].y), rw, static_cast<float>(x[i].y));
     }
 }
 
@@ -288,12 +291,12 @@ __device__ __forceinline__ void load_norm_batch(u4 (&xv)[kXB], u4 (&rv)[kXB], u4
 }
 
 template <bool ONE_ROW>
-__device__ __forceinline__ void norm_group_sums(float* gsum, const u4 (&xv)[kXB], const u4 (&rv)[kXB], bool has_r,
+__device__ __forceinline__ void norm_group_sums(float* gsum, const u4 (&xv)[kXB], const u4 (&rv)[kXB], float rw,
                                                 const XSlice& xs, int G, int f0, int lane) {
 #pragma unroll
     for (int j = 0; j < kXB; ++j) {
         float sv[8];
-        norm_sum(xv[j], rv[j], has_r, sv);
+        norm_sum(xv[j], rv[j], rw, sv);
         const float q = row16_sum(sumsq8(sv));
         const int f = f0 + 64 * j;
         const XPos p = x_pos<ONE_ROW>(xs, f);
@@ -304,19 +307,22 @@ __device__ __forceinline__ void norm_group_sums(float* gsum, const u4 (&xv)[kXB]
 template <bool BIASED, bool ONE_ROW, int MR>
 __device__ __forceinline__ void norm_store_batch(u4* smem, const DecodeLds& l, float2* corr, int kx, const XSlice& xs,
                                                  const u4 (&xv)[kXB], const u4 (&rv)[kXB], const u4 (&wv)[kXB],
-                                                 bool has_r, const float (&rstd)[MR], int f0) {
+                                                 float rw, const float (&rstd)[MR], int f0) {
 #pragma unroll
     for (int j = 0; j < kXB; ++j) {
         const int f = f0 + 64 * j;
         const XPos p = x_pos<ONE_ROW>(xs, f);
-        float sv[8], gv[8];
-        norm_sum(xv[j], rv[j], has_r, sv);
+        float sv[8];
+        norm_sum(xv[j], rv[j], rw, sv);
         float rs = rstd[0];
 #pragma unroll
         for (int m = 1; m < MR; ++m) rs = p.m == m ? rstd[m] : rs;
-        chunk_to_f32(wv[j], gv);
+        const h2 g[4] = {bitcast<h2>(wv[j].x), bitcast<h2>(wv[j].y), bitcast<h2>(wv[j].z), bitcast<h2>(wv[j].w)};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sv[i] = sv[i] * rs * gv[i];
+        for (int i = 0; i < 4; ++i) {  // (s rstd) g: the product with the fp16 g as an fma with -0 (exact)
+            sv[2 * i] = __builtin_fmaf(sv[2 * i] * rs, static_cast<float>(g[i].x), -0.0f);
+            sv[2 * i + 1] = __builtin_fmaf(sv[2 * i + 1] * rs, static_cast<float>(g[i].y), -0.0f);
+        }
         store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, f32_to_chunk(sv), f);
     }
 }
@@ -331,13 +337,14 @@ __device__ __forceinline__ void stage_x_norm(u4* smem, const DecodeLds& l, float
     float* gsum = reinterpret_cast<float*>(smem + l.norm);  // [M][G]
     const bool has_r = nin.r != nullptr;
     const u4* rg = has_r ? reinterpret_cast<const u4*>(nin.r) : xg;
+    const float rw = has_r ? 1.0f : 0.0f;
     const u4* wg = reinterpret_cast<const u4*>(nin.w);
     if (xs.n > 0) {
-        norm_group_sums<ONE_ROW>(gsum, fx, fr, has_r, xs, G, lane, lane);
+        norm_group_sums<ONE_ROW>(gsum, fx, fr, rw, xs, G, lane, lane);
         for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {  // wavefront-uniform trip count
             u4 xv[kXB], rv[kXB], wv[kXB];
             load_norm_batch<ONE_ROW, false>(xv, rv, wv, xg, rg, wg, kx, xs, f0);
-            norm_group_sums<ONE_ROW>(gsum, xv, rv, has_r, xs, G, f0, lane);
+            norm_group_sums<ONE_ROW>(gsum, xv, rv, rw, xs, G, f0, lane);
         }
     }
     __syncthreads();
@@ -346,11 +353,11 @@ __device__ __forceinline__ void stage_x_norm(u4* smem, const DecodeLds& l, float
     for (int m = 0; m < MR; ++m)
         rstd[m] = m < M ? norm_rstd(gsum + m * G, G, K, nin.eps, lane) : 0.0f;  // wavefront-uniform branch
     if (xs.n > 0) {
-        norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, fx, fr, fw, has_r, rstd, lane);
+        norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, fx, fr, fw, rw, rstd, lane);
         for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {
             u4 xv[kXB], rv[kXB], wv[kXB];
             load_norm_batch<ONE_ROW, true>(xv, rv, wv, xg, rg, wg, kx, xs, f0);
-            norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, xv, rv, wv, has_r, rstd, f0);
+            norm_store_batch<BIASED, ONE_ROW, MR>(smem, l, corr, kx, xs, xv, rv, wv, rw, rstd, f0);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -372,7 +379,7 @@ __device__ __forceinline__ void write_residual(const u4* xg, const NormIn& nin, 
             const int f = f0 + 64 * j;
             const XPos p = x_pos<ONE_ROW>(xs, f);
             float sv[8];
-            norm_sum(xv[j], rv[j], true, sv);
+            norm_sum(xv[j], rv[j], 1.0f, sv);
             if (f < xs.n) rog[static_cast<int64_t>(p.m) * kx + xs.c0 + p.c] = f32_to_chunk(sv);
         }
     }
