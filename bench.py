@@ -207,8 +207,8 @@ def decode_step(torch, dev) -> dict:
 def main() -> int:
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {a.gpus} is not supported (this path is data-parallel per "
-              "replica; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {a.gpus} is not supported (the W4A16 linear runs on one GPU's "
+              "share of the weights; sharding splits N or K across GPUs outside this op)", file=sys.stderr)
         return 2
     import torch
 
