@@ -233,3 +233,71 @@ def test_graph_runner_matches_eager_buckets():
                 _close(got, _oracle_step(w, ids), 0.02, ("runner", b))
     with pytest.raises(ValueError):
         runner.run(list(range(9)))
+
+
+def _write_checkpoint(path, cfg: tmodel.DecoderConfig, seed: int):
+    """A synthetic AutoAWQ checkpoint of ``cfg`` (separate q/k/v and gate/up tensors, as AutoAWQ
+    writes them) and the numpy weights of the step built from it."""
+    import json
+
+    from safetensors.torch import save_file
+
+    rng = np.random.default_rng(seed)
+    t, w = {}, {"layers": []}
+    q, kv = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    h, inter = cfg.hidden_size, cfg.intermediate_size
+    i = 0
+    for li in range(cfg.num_layers):
+        raw = {}
+        for name, (k, n) in (("self_attn.q_proj", (h, q)), ("self_attn.k_proj", (h, kv)), ("self_attn.v_proj", (h, kv)),
+                             ("self_attn.o_proj", (q, h)), ("mlp.gate_proj", (h, inter)), ("mlp.up_proj", (h, inter)),
+                             ("mlp.down_proj", (inter, h))):
+            qw, qz, s, _, _ = o.random_awq(k, n, seed=seed * 100 + i)
+            i += 1
+            raw[name] = (qw, qz, s)
+            for suffix, arr in (("qweight", qw), ("qzeros", qz), ("scales", s)):
+                t[f"model.layers.{li}.{name}.{suffix}"] = torch.from_numpy(np.ascontiguousarray(arr))
+        n1 = (1.0 + (rng.random(h) - 0.5) * 0.2).astype(np.float16)
+        n2 = (1.0 + (rng.random(h) - 0.5) * 0.2).astype(np.float16)
+        t[f"model.layers.{li}.input_layernorm.weight"] = torch.from_numpy(n1)
+        t[f"model.layers.{li}.post_attention_layernorm.weight"] = torch.from_numpy(n2)
+        deq = {k: o.dequant(*v) for k, v in raw.items()}
+        w["layers"].append({"qkv": np.concatenate([deq["self_attn.q_proj"], deq["self_attn.k_proj"],
+                                                   deq["self_attn.v_proj"]]),
+                            "o": deq["self_attn.o_proj"],
+                            "gate_up": np.concatenate([deq["mlp.gate_proj"], deq["mlp.up_proj"]]),
+                            "down": deq["mlp.down_proj"], "n1": n1, "n2": n2})
+    emb = (rng.standard_normal((cfg.vocab_size, h))).astype(np.float16)
+    fn = (1.0 + (rng.random(h) - 0.5) * 0.2).astype(np.float16)
+    t["model.embed_tokens.weight"] = torch.from_numpy(emb)
+    t["model.norm.weight"] = torch.from_numpy(fn)
+    save_file(t, str(path / "model.safetensors"))
+    (path / "config.json").write_text(json.dumps({"quantization_config": {
+        "quant_method": "awq", "bits": 4, "group_size": 128, "zero_point": True, "version": "gemm"}}))
+    w.update(emb=emb, head=emb, norm=fn)  # tied embeddings: the logits head is the embedding
+    return w
+
+
+@pytest.mark.gpu
+def test_checkpoint_to_graph_runner(tmp_path):
+    """AutoAWQ checkpoint -> tandem_amd.loader -> tandem_amd.model (tied embeddings, as Qwen3-1.7B)
+    -> bucketed HIP graphs: logits against the oracle's step on the checkpoint's weights."""
+    import json
+
+    from tandem_amd import loader
+
+    cfg = tmodel.DecoderConfig(hidden_size=512, intermediate_size=1024, num_heads=4, num_kv_heads=2, head_dim=128,
+                               num_layers=2, vocab_size=777, tie_word_embeddings=True)
+    w = _write_checkpoint(tmp_path, cfg, seed=5)
+    quant = loader.QuantConfig.from_dict(json.loads((tmp_path / "config.json").read_text())["quantization_config"])
+    model = tmodel.DecoderModel(cfg, quant)
+    loader.load_weights(model, str(tmp_path))
+    tmodel.prepare(model, torch.device("cuda", 0), torch.cuda.get_device_name())
+    runner = decode_graph.DecodeGraphRunner(model, max_bs=4, device=torch.device("cuda", 0))
+    global TINY
+    saved, TINY = TINY, cfg  # _oracle_step reads the shapes from TINY
+    try:
+        for ids in ([3], [776, 0, 5]):
+            _close(runner.run(ids), _oracle_step(w, np.array(ids)), 0.02, ("checkpoint", ids))
+    finally:
+        TINY = saved
