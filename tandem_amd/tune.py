@@ -29,6 +29,10 @@ MODELS = {
     "qwen3-1.7b": {"qkv": (2048, 4096), "o": (2048, 2048), "gate_up": (2048, 12288), "down": (6144, 2048),
                    "lm_head": (2048, 151936)},
     "qwen3-0.6b": {"qkv": (1024, 4096), "lm_head": (1024, 151936)},
+    # other common AWQ checkpoints (hidden, intermediate, heads / kv heads x 128)
+    "qwen3-4b": {"qkv": (2560, 6144), "o": (4096, 2560), "gate_up": (2560, 19456), "down": (9728, 2560)},
+    "qwen3-14b": {"qkv": (5120, 7168), "o": (5120, 5120), "gate_up": (5120, 34816), "down": (17408, 5120)},
+    "llama3-8b": {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 28672), "down": (14336, 4096)},
 }
 DENSE = ("lm_head",)  # fp16 projections (kinds dense16 / torch16); the others are W4A16
 
