@@ -163,11 +163,13 @@ W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
 # LDS ring, SPLITS: split-K of every tile, or 0: of the last, partial wave of tiles only), or
 # ("mma", warps_k, unroll, ntile): the streaming matrix-core kernel of the decode path, whose 16-token
 # batch tiles cover M <= 64 (bandwidth-bound batches), or None: dequantize to float16 +
-# torch.matmul. Shapes without an entry use DEFAULT_GEMM.
+# torch.matmul. Shapes without an entry use DEFAULT_GEMM, which ends like every measured gfx950
+# ladder: past M = 1024 the dequantize + hipBLASLt pair beats the fused GEMM (by ~30% at M = 4096 on
+# the Qwen3-8B shapes), since the one-off dequant is small next to the product there.
 # TANDEM_W4_GEMM=0: always dequantize + torch.matmul (python/tandem/layers/awq.py:163-186).
 W4Gemm = tuple
 DEFAULT_GEMM: tuple[tuple[int, W4Gemm | None], ...] = (
-    (64, ("mma", 8, 1, 1)), (1 << 30, (4, 2, 4, 1, 2, 0)))
+    (64, ("mma", 8, 1, 1)), (1024, (4, 2, 4, 1, 2, 0)), (1 << 30, None))
 W4_GEMM_KERNELS: dict[str, dict[tuple, tuple[tuple[int, W4Gemm | None], ...]]] = {
     MI355X: GFX950_GEMM,
     GFX950: GFX950_GEMM,

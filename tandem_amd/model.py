@@ -19,8 +19,8 @@ kernel, so a captured step has the real launch sequence of a decoder layer aroun
 Projections are W4Linear (AutoAWQ checkpoints) or nn.Linear (fp16 checkpoints); ``prepare`` moves
 the model to the GPU, repacks the W4 layers and routes the fp16 projections and the logits head
 through layers/gemv16.py's table. Norms run on tw4_rms_norm / tw4_add_rms_norm, or inside the W4
-qkv_proj / gate_up_proj kernels where W4Linear.forward_norm can fuse them (the decode GEMV and the
-matrix-core decode kernel: a norm kernel fewer before each, the same bits).
+qkv_proj / gate_up_proj kernels where W4Linear.forward_norm fuses them (the decode GEMV at the
+batch sizes it runs: a norm kernel fewer before each, the same bits).
 """
 
 from __future__ import annotations
