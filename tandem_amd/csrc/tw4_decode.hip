@@ -40,7 +40,7 @@ namespace tw4 {
 template <int U, int NT>
 struct WeightSet {  // one chunk's weight blocks and group parameters, per lane
     u4 w[U][NT];
-    uint32_t p[U][NT];  // the row's scale (lanes of rows kb = 0, 2) or zero (kb = 1, 3): see scale_zero
+    uint16_t p[U][NT];  // the row's scale (lanes of rows kb = 0, 2) or zero (kb = 1, 3): see scale_zero
 };
 
 // Lanes 16 kb + r of even kb load row r's scale, of odd kb its zero: one 2-byte load per lane and
@@ -184,10 +184,10 @@ __device__ __forceinline__ u4 x_chunk(const u4* xg, int kx, const XSlice& xs, XP
     return xg[static_cast<int64_t>(p.m) * kx + xs.c0 + p.c];
 }
 
-template <bool ONE_ROW>
-__device__ __forceinline__ void load_x_batch(u4 (&v)[kXB], const u4* xg, int kx, const XSlice& xs, int f0) {
+template <bool ONE_ROW, int XB = kXB>
+__device__ __forceinline__ void load_x_batch(u4 (&v)[XB], const u4* xg, int kx, const XSlice& xs, int f0) {
 #pragma unroll
-    for (int j = 0; j < kXB; ++j) v[j] = x_chunk(xg, kx, xs, x_pos<ONE_ROW>(xs, f0 + 64 * j));
+    for (int j = 0; j < XB; ++j) v[j] = x_chunk(xg, kx, xs, x_pos<ONE_ROW>(xs, f0 + 64 * j));
 }
 
 // Flat chunk f into LDS. BIASED: as x' (pairs k = 8 j + 2, 3 and 8 j + 6, 7 divided by 16: exact, a
@@ -229,16 +229,16 @@ __device__ __forceinline__ void store_x_chunk(u4* smem, const DecodeLds& l, floa
 
 // Stores the first batch (already loaded), then loads and stores the rest of the slice batch by
 // batch; ends with the wavefront's LDS writes ordered before its reads.
-template <bool BIASED, bool ONE_ROW>
+template <bool BIASED, bool ONE_ROW, int XB = kXB>
 __device__ __forceinline__ void stage_x(u4* smem, const DecodeLds& l, float2* corr, const u4* xg, int kx,
-                                        const XSlice& xs, const u4 (&first)[kXB], int lane) {
+                                        const XSlice& xs, const u4 (&first)[XB], int lane) {
 #pragma unroll
-    for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, first[j], lane + 64 * j);
-    for (int f0 = lane + 64 * kXB; f0 - lane < xs.n; f0 += 64 * kXB) {  // wavefront-uniform trip count
-        u4 v[kXB];
-        load_x_batch<ONE_ROW>(v, xg, kx, xs, f0);
+    for (int j = 0; j < XB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, first[j], lane + 64 * j);
+    for (int f0 = lane + 64 * XB; f0 - lane < xs.n; f0 += 64 * XB) {  // wavefront-uniform trip count
+        u4 v[XB];
+        load_x_batch<ONE_ROW, XB>(v, xg, kx, xs, f0);
 #pragma unroll
-        for (int j = 0; j < kXB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, v[j], f0 + 64 * j);
+        for (int j = 0; j < XB; ++j) store_x_chunk<BIASED, ONE_ROW>(smem, l, corr, kx, xs, v[j], f0 + 64 * j);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -478,11 +478,11 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
         load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
         __builtin_amdgcn_sched_barrier(0);
         stage_x_norm<true, M == 1, M>(smem, l, corr, xg, kx, xsl, nin, M, G, K, fx, fr, fw, lane);
-    } else if (nch > 0) {
+    } else {  // unconditional as well: a branch here makes the compiler wait for the whole first chunk
         u4 xfirst[kXB];
         load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
         __builtin_amdgcn_sched_barrier(0);
-        load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+        load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
         __builtin_amdgcn_sched_barrier(0);
         stage_x<true, M == 1>(smem, l, corr, xg, kx, xsl, xfirst, lane);
     }
@@ -671,11 +671,11 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
     const u4* xg = reinterpret_cast<const u4*>(x);
     const XSlice xsl = x_slice(gb, ge, M);
     WeightSetM<U, NT> a, b;
-    if (nch > 0) {
+    {  // no branch around the first loads (see gemv_kernel); an empty slice reads valid addresses
         u4 xfirst[kXB];
         load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
         __builtin_amdgcn_sched_barrier(0);
-        load_chunk_m<U, NT>(a, ts, s16, z16, gb, ge - 1, kb);
+        load_chunk_m<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0), kb);
         __builtin_amdgcn_sched_barrier(0);
         stage_x<true, M == 1>(smem, l, corr, xg, kx, xsl, xfirst, lane);
         group_corr<M>(corr, gcorr, G, gb, ge, lane);
@@ -740,13 +740,20 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
 // MT batch tiles of 16 columns (M <= 16 MT): lane (kb, r) feeds B column r of tile b = token
 // 16 b + r, and D tile (t, b) holds rows 4 kb + i of that token. Each dequantized A fragment feeds
 // MT MFMAs.
-template <bool PF, bool XLDS, int U, int NT, int MT>
+// Where the mma kernel reads its B fragments (x): straight from global memory at the start of each
+// chunk, or from an LDS image staged once per wavefront, in batches of 2 (kXLds) or 8 (kXLdsWide)
+// 16-byte chunks per lane. A batch is loaded before the first weight chunk; a later batch waits for
+// that chunk too (loads retire in order), so the host takes the wide batch where a lane's share of the
+// slice is more than 2 chunks and the narrow one where the extra, repeated loads would cost.
+enum XMode { kXGlobal = 0, kXLds = 1, kXLdsWide = 2 };
+
+template <bool PF, int XM, int U, int NT, int MT>
 __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
                                           const uint16_t* s16, const uint16_t* z16, const u4* smem, const DecodeLds& l,
                                           const h8* const (&xl)[MT], int xrow, f4 (&acc)[NT][MT], int g0, int ge,
                                           int kb, uint32_t magic) {
-    h8 xb[XLDS ? 1 : U][4][MT];
-    if constexpr (!XLDS) {  // issued first: waiting for x never waits for the prefetch below
+    h8 xb[XM == kXGlobal ? U : 1][4][MT];
+    if constexpr (XM == kXGlobal) {  // issued first: waiting for x never waits for the prefetch below
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int g = min(g0 + u, ge - 1);
@@ -775,7 +782,7 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
             h8 xv[MT];
 #pragma unroll
             for (int b = 0; b < MT; ++b) {
-                if constexpr (XLDS)
+                if constexpr (XM != kXGlobal)
                     xv[b] = bitcast<h8>(smem[xrow * l.xs + 16 * g + 4 * kb + s]);
                 else
                     xv[b] = xb[u][s][b];
@@ -790,10 +797,12 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
     }
 }
 
-template <int WK, int U, int NT, int MT, bool XLDS, bool NORM = false>
+template <int WK, int U, int NT, int MT, int XM, bool NORM = false>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                      h1* __restrict__ y, int M, int N, int K, int act, NormIn nin) {
+    constexpr bool XLDS = XM != kXGlobal;
+    constexpr int XB = XM == kXLdsWide ? 8 : 2;
     static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
     static_assert(!NORM || XLDS, "the fused norm stages x in LDS");
     if constexpr (U * MT > 4 && MT > 1) {
@@ -830,16 +839,16 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
             load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
             __builtin_amdgcn_sched_barrier(0);
             stage_x_norm<false, false, kNormMaxRows>(smem, l, nullptr, xg, kx, xsl, nin, M, G, K, fx, fr, fw, lane);
-        } else if (nch > 0) {
-            u4 xfirst[kXB];
-            load_x_batch<false>(xfirst, xg, kx, xsl, lane);
+        } else {  // no branch around the first loads (see gemv_kernel)
+            u4 xfirst[XB];
+            load_x_batch<false, XB>(xfirst, xg, kx, xsl, lane);
             __builtin_amdgcn_sched_barrier(0);
-            load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+            load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
             __builtin_amdgcn_sched_barrier(0);
-            stage_x<false, false>(smem, l, nullptr, xg, kx, xsl, xfirst, lane);
+            stage_x<false, false, XB>(smem, l, nullptr, xg, kx, xsl, xfirst, lane);
         }
     } else {
-        if (nch > 0) load_chunk<U, NT>(a, ts, s16, z16, gb, ge - 1);
+        load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
     }
 
     f4 acc[NT][MT];
@@ -849,14 +858,14 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
     for (; i + 2 < nch; i += 2) {
-        mma_chunk<true, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<true, XLDS, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
     }
     if (i + 2 == nch) {
-        mma_chunk<true, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<false, XLDS, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
     } else if (i + 1 == nch) {
-        mma_chunk<false, XLDS, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
     }
     if constexpr (NORM) write_residual<false>(xg, nin, kx, xsl, lane);
     if (WK > 1) {
@@ -951,11 +960,12 @@ int decode_prepare(int dev) {
     if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<2, WK, U, T>);             \
     if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<3, WK, U, T>);             \
     if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<4, WK, U, T>);             \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true>);         \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, true, true>);   \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, false>);        \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, false>);        \
-    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, false>);
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds>);         \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds, true>);   \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLdsWide>);     \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXGlobal>);      \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, kXGlobal>);      \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, kXGlobal>);
     TW4_DECODE_CONFIGS(TW4_ATTR)
 #undef TW4_ATTR
 #undef TW4_ATTR_GEMV
@@ -1096,6 +1106,8 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
                 "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
     const int tiles = (N + 15) >> 4;
     const bool xlds = mt == 1 && static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+    const int gw = ((K >> 7) + warps_k - 1) / max(warps_k, 1);
+    const bool wide = M * gw > 8;  // a lane's share of the staged slice, M gw / 4 chunks, is more than 2
     TW4_REQUIRE(!nin || xlds, TW4_ECONFIG,
                 "mma: the fused norm stages x in LDS: M (K + 8) 2 bytes <= %d (M = %d, K = %d)", kXLdsLimit, M, K);
     const NormIn none{nullptr, nullptr, nullptr, 0.0f};
@@ -1105,15 +1117,17 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
             16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * mt * 64, nin != nullptr).total); \
         const unsigned grid = (tiles + T - 1) / T;                                                             \
         if (nin)                                                                                               \
-            mma_kernel<WK, U, T, 1, true, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin); \
+            mma_kernel<WK, U, T, 1, kXLds, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin); \
+        else if (xlds && wide)                                                                                 \
+            mma_kernel<WK, U, T, 1, kXLdsWide><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
         else if (xlds)                                                                                         \
-            mma_kernel<WK, U, T, 1, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 1, kXLds><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
         else if (mt == 1)                                                                                      \
-            mma_kernel<WK, U, T, 1, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 1, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
         else if (mt == 2)                                                                                      \
-            mma_kernel<WK, U, T, 2, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 2, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
         else                                                                                                   \
-            mma_kernel<WK, U, T, 4, false><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 4, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
         TW4_LAUNCH_CHECK("mma: launch");                                                                       \
         return TW4_OK;                                                                                         \
     }
