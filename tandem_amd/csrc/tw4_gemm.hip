@@ -326,7 +326,8 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
 template <int U, int NT>
 struct StreamSet {
     u4 w[U][NT];
-    uint32_t p[U][NT];  // scale (even kb) or zero (odd kb) of the lane's row
+    uint16_t p[U][NT];  // scale (even kb) or zero (odd kb) of the lane's row (16 bits: no zero-extension
+                        // that the compiler could place, with a wait for the load, before the main loop)
 };
 
 template <int MT, int NT, int WN, int WK, int U>
@@ -417,29 +418,6 @@ __global__ void __launch_bounds__(WN * WK * 64) stream_kernel(
     const int rows = min(C::BM, M - m0);  // x rows that exist
     const int wt0 = (nblk * WN + wn) * NT;
 
-    // stage x[m0 .. m0 + rows - 1][groups glo .. ghi - 1]: flat chunk f -> (row f / (16 R), chunk
-    // f % (16 R)); XB loads in flight per thread before their stores
-    {
-        const int r16 = 16 * R, total = rows * r16;
-        const uint32_t magic16 = 0xFFFFFFFFu / static_cast<uint32_t>(r16) + 1u;  // f / r16 = umulhi(f, magic16)
-        const u4* xg = reinterpret_cast<const u4*>(x);
-        const int kx = K >> 3;
-        for (int f0 = tid; f0 - tid < total; f0 += C::XB * C::THREADS) {  // workgroup-uniform trip count
-            u4 v[C::XB];
-            int dst[C::XB];
-#pragma unroll
-            for (int i = 0; i < C::XB; ++i) {
-                const int f = min(f0 + i * C::THREADS, total - 1);  // past the end: repeat the last chunk
-                const int rho = static_cast<int>(__umulhi(static_cast<uint32_t>(f), magic16));
-                const int c = f - rho * r16;
-                v[i] = xg[static_cast<int64_t>(m0 + rho) * kx + 16 * glo + c];
-                dst[i] = (rho * R + (c >> 4)) * 16 + ((c & 15) ^ (rho & 15));
-            }
-#pragma unroll
-            for (int i = 0; i < C::XB; ++i) lds[dst[i]] = v[i];
-        }
-    }
-
     // this wavefront's groups and weight / parameter streams
     const int gw = (R + WK - 1) / WK, gb = glo + min(wk * gw, R), ge = glo + min(wk * gw + gw, R);
     const int nch = (ge - gb + U - 1) / U;
@@ -464,8 +442,41 @@ __global__ void __launch_bounds__(WN * WK * 64) stream_kernel(
     }
     const uint32_t magic = magic_reg();
 
+    // stage x[m0 .. m0 + rows - 1][groups glo .. ghi - 1]: flat chunk f -> (row f / (16 R), chunk
+    // f % (16 R)); XB loads in flight per thread before their stores. The wavefront's first weight
+    // chunk is issued right behind the first x batch, so its memory latency overlaps the staging
+    // (loads retire in order: waiting for that batch never waits for the weights). No branch sits
+    // around these loads; an empty group range loads a valid block that is never used.
     StreamSet<U, NT> a, b2;
-    if (nch > 0) stream_load<U, NT>(a, wb, pb, srows, gb, ge - 1);
+    {
+        const int r16 = 16 * R, total = rows * r16;
+        const uint32_t magic16 = 0xFFFFFFFFu / static_cast<uint32_t>(r16) + 1u;  // f / r16 = umulhi(f, magic16)
+        const u4* xg = reinterpret_cast<const u4*>(x);
+        const int kx = K >> 3;
+        auto load_batch = [&](int f0, u4 (&v)[C::XB], int (&dst)[C::XB]) {
+#pragma unroll
+            for (int i = 0; i < C::XB; ++i) {
+                const int f = min(f0 + i * C::THREADS, total - 1);  // past the end: repeat the last chunk
+                const int rho = static_cast<int>(__umulhi(static_cast<uint32_t>(f), magic16));
+                const int c = f - rho * r16;
+                v[i] = xg[static_cast<int64_t>(m0 + rho) * kx + 16 * glo + c];
+                dst[i] = (rho * R + (c >> 4)) * 16 + ((c & 15) ^ (rho & 15));
+            }
+        };
+        u4 v[C::XB];
+        int dst[C::XB];
+        load_batch(tid, v, dst);
+        __builtin_amdgcn_sched_barrier(0);
+        stream_load<U, NT>(a, wb, pb, srows, gb, max(ge - 1, 0));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < C::XB; ++i) lds[dst[i]] = v[i];
+        for (int f0 = tid + C::XB * C::THREADS; f0 - tid < total; f0 += C::XB * C::THREADS) {  // uniform trip count
+            load_batch(f0, v, dst);
+#pragma unroll
+            for (int i = 0; i < C::XB; ++i) lds[dst[i]] = v[i];
+        }
+    }
     __syncthreads();  // x staged
 
     f4 acc[NT][MT];
