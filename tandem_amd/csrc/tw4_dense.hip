@@ -9,6 +9,10 @@
 // 16 bytes per 16 weight bytes (x chunks are read once per row block and shared by its RB rows).
 // Each lane accumulates its chunks with v_dot2_f32_f16; a row's 64 partial sums are added with
 // DPP (within rows of 16 lanes) and two permlane swaps, and lane 0 writes the RB x M results.
+//
+// For M = 5 .. 8 the v_dot2 form reads M x 16 bytes of x from LDS per 16 weight bytes, which makes
+// it LDS-bound; the matrix-core form (rows_inflight = 16) takes 16-row tiles of w as the A operand
+// of v_mfma_f32_16x16x32_f16 and x as B, so one 16-byte B fragment serves 16 rows.
 #include "tw4_common.h"
 
 namespace tw4 {
@@ -110,8 +114,108 @@ __global__ void __launch_bounds__(256) dense_gemv_kernel(const h1* __restrict__ 
     }
 }
 
+// ------------------------------------------------------------------------- matrix cores, M <= 8
+// A wavefront owns rows_per_wave rows (whole 16-row tiles) and walks them tile by tile, each over
+// all of K in chunks of 128 k. Lane (kb, r) loads, for word s = 0..3 of a chunk, the 16 bytes of
+// row r at k = 128 c + 8 (4 s + kb) .. + 7 (one instruction per s: 64 contiguous bytes per row), and
+// feeds them as A row r; the B fragment of token r is x at the same k from LDS, so each MFMA sums 32
+// distinct k of the chunk. The next chunk (possibly the next tile's first) is in flight in a second
+// register set while the current one is multiplied. D holds rows 4 kb + i of token r in lane (kb, r).
+// x: 8 token rows in LDS (rows past M repeat row M - 1; B columns r >= 8 read row 7 and feed D
+// columns that are never stored), row stride K / 8 + 1 chunks so the 16 rows of a fragment read hit
+// different banks. Staged once per workgroup, its loads issued before the first weight chunk.
+constexpr int kMmaWaves = 8;  // wavefronts per workgroup of the matrix-core form (one x copy each)
+
+struct ChunkSet {
+    u4 w[4];
+};
+
+// Plain (cached) loads: an instruction reads 64 bytes of each of 16 rows, half of a 128-byte line whose
+// other half the next word's load reads (with non-temporal loads the tile ran 2 % slower).
+__device__ __forceinline__ void load_chunk16(ChunkSet& cs, const u4* wrow, int c, int kb) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) cs.w[s] = wrow[16 * c + 4 * s + kb];
+}
+
+template <bool PF>
+__device__ __forceinline__ void mma16_step(const ChunkSet& cur, ChunkSet& nxt, const u4* nrow, int nc, const u4* xr,
+                                           int c, int kb, f4& acc) {
+    if constexpr (PF) load_chunk16(nxt, nrow, nc, kb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        acc = mfma16x16x32(bitcast<h8>(cur.w[s]), bitcast<h8>(xr[16 * c + 4 * s + kb]), acc);
+}
+
+// J = K / 512 x chunks per thread for the staging (K <= 4096: at most 8)
+template <int J>
+__global__ void __launch_bounds__(kMmaWaves * 64) dense_mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
+                                                                   h1* __restrict__ y, int Mx, int N,
+                                                                   int rows_per_wave) {
+    extern __shared__ u4 xs[];
+    constexpr int kc = 64 * J;  // 16-byte chunks per row of x and w
+    constexpr int C = kc / 16;  // 128-k chunks per row (even)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, kb = lane >> 4;
+    const int row0 = (blockIdx.x * kMmaWaves + wave) * rows_per_wave;
+    const int tiles = (max(min(rows_per_wave, N - row0), 0) + 15) >> 4;  // the last one may be partial
+    const int last_tile = max(tiles - 1, 0);
+    auto wrow = [&](int t) {  // this lane's row of tile t (rows past N read row N - 1)
+        return w + static_cast<int64_t>(min(row0 + 16 * t + r, N - 1)) * kc;
+    };
+
+    // x staging: thread i takes chunks i, i + 512, ... (J of them) of the 8 x kc token-row image
+    const u4* xg = reinterpret_cast<const u4*>(x);
+    u4 xv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int f = threadIdx.x + kMmaWaves * 64 * j;  // < 8 kc
+        const int m = f / kc;                            // kc is a power of two
+        xv[j] = xg[static_cast<int64_t>(min(m, Mx - 1)) * kc + (f - m * kc)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    ChunkSet a, b;
+    load_chunk16(a, wrow(0), 0, kb);  // tiles == 0: a valid row, never used
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int f = threadIdx.x + kMmaWaves * 64 * j;
+        const int m = f / kc;
+        xs[m * (kc + 1) + (f - m * kc)] = xv[j];
+    }
+    __syncthreads();
+
+    const u4* xr = xs + min(r, 7) * (kc + 1);
+    for (int t = 0; t < tiles; ++t) {
+        const u4* cr = wrow(t);
+        const u4* nr = wrow(min(t + 1, last_tile));  // the last tile prefetches its own first chunk: unused
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < C - 2; c += 2) {
+            mma16_step<true>(a, b, cr, c + 1, xr, c, kb, acc);
+            mma16_step<true>(b, a, cr, c + 2, xr, c + 1, kb, acc);
+        }
+        mma16_step<true>(a, b, cr, C - 1, xr, C - 2, kb, acc);
+        mma16_step<true>(b, a, nr, 0, xr, C - 1, kb, acc);
+        const int n = row0 + 16 * t + 4 * kb;
+        if (r < Mx && n < N) {
+            h1* yp = y + static_cast<int64_t>(r) * N + n;
+            if (n + 3 < N && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+                *reinterpret_cast<h4*>(yp) = h4{static_cast<h1>(acc.x), static_cast<h1>(acc.y),
+                                                static_cast<h1>(acc.z), static_cast<h1>(acc.w)};
+            } else {
+                const float v[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (n + i < N) yp[i] = static_cast<h1>(v[i]);
+            }
+        }
+    }
+}
+
 // Compiled (rows in flight RB, rows per wavefront) configurations.
 #define TW4_DENSE_CONFIGS(X) X(1, 16) X(1, 32) X(2, 16) X(2, 32) X(2, 64) X(4, 32) X(4, 64)
+// Matrix-core form (rows_inflight 16): rows per wavefront, whole 16-row tiles.
+#define TW4_DENSE_MMA_CONFIGS(X) X(16, 16) X(16, 32) X(16, 64) X(16, 128)
 
 template <int M, int RB, int J>
 int dense_launch(const h1* x, const u4* w, h1* y, int Mx, int N, int rows_per_wave, hipStream_t st) {
@@ -130,6 +234,28 @@ int dense_by_k(const h1* x, const u4* w, h1* y, int Mx, int N, int K, int rows_p
         case 2: return dense_launch<M, RB, 2>(x, w, y, Mx, N, rows_per_wave, st);
         case 4: return dense_launch<M, RB, 4>(x, w, y, Mx, N, rows_per_wave, st);
         case 8: return dense_launch<M, RB, 8>(x, w, y, Mx, N, rows_per_wave, st);
+        default: break;
+    }
+    tw4host::set_error("gemv_f16: K = %d (K in 512, 1024, 2048, 4096)", K);
+    return TW4_EINVAL;
+}
+
+template <int J>
+int dense_mma_launch(const h1* x, const u4* w, h1* y, int Mx, int N, int rows_per_wave, hipStream_t st) {
+    const int64_t waves = (static_cast<int64_t>(N) + rows_per_wave - 1) / rows_per_wave;
+    const unsigned grid = static_cast<unsigned>((waves + kMmaWaves - 1) / kMmaWaves);
+    const size_t lds = static_cast<size_t>(8) * (64 * J + 1) * 16;  // <= 65.7 KB
+    dense_mma_kernel<J><<<grid, kMmaWaves * 64, lds, st>>>(x, w, y, Mx, N, rows_per_wave);
+    TW4_LAUNCH_CHECK("gemv_f16: launch");
+    return TW4_OK;
+}
+
+int dense_mma(const h1* x, const u4* w, h1* y, int M, int N, int K, int rows_per_wave, hipStream_t st) {
+    switch (K >> 9) {
+        case 1: return dense_mma_launch<1>(x, w, y, M, N, rows_per_wave, st);
+        case 2: return dense_mma_launch<2>(x, w, y, M, N, rows_per_wave, st);
+        case 4: return dense_mma_launch<4>(x, w, y, M, N, rows_per_wave, st);
+        case 8: return dense_mma_launch<8>(x, w, y, M, N, rows_per_wave, st);
         default: break;
     }
     tw4host::set_error("gemv_f16: K = %d (K in 512, 1024, 2048, 4096)", K);
@@ -166,6 +292,10 @@ extern "C" int tw4_gemv_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, i
     if (rows_inflight == RB && rows_per_wave == RPW) return dense_by_m<RB>(xp, wp, yp, M, N, K, RPW, st);
     TW4_DENSE_CONFIGS(TW4_DENSE_CASE)
 #undef TW4_DENSE_CASE
+#define TW4_DENSE_MMA_CASE(RB, RPW) \
+    if (rows_inflight == RB && rows_per_wave == RPW) return dense_mma(xp, wp, yp, M, N, K, RPW, st);
+    TW4_DENSE_MMA_CONFIGS(TW4_DENSE_MMA_CASE)
+#undef TW4_DENSE_MMA_CASE
     tw4host::set_error("gemv_f16: unsupported rows in flight / rows per wavefront %d / %d", rows_inflight,
                        rows_per_wave);
     return TW4_ECONFIG;
@@ -180,6 +310,7 @@ extern "C" int tw4_gemv_f16_configs(int* out, int max_configs) {
     }                                     \
     ++n;
     TW4_DENSE_CONFIGS(TW4_LIST)
+    TW4_DENSE_MMA_CONFIGS(TW4_LIST)
 #undef TW4_LIST
     return n;
 }

@@ -76,12 +76,13 @@ def test_gemv_every_config(k):
 
 @pytest.mark.gpu
 def test_lm_head_shape_through_linear():
-    """The Qwen3-8B fp16 lm_head shape (151936 x 4096) through linear() with a table entry."""
+    """The Qwen3-8B fp16 lm_head shape (151936 x 4096) through linear() with a table entry, on the
+    v_dot2 form (M = 1, 3) and the matrix-core form (M = 5, 8)."""
     dev = "cuda"
     g = torch.Generator(device=dev).manual_seed(1)
     w = (torch.randn(151936, 4096, device=dev, generator=g) * 0.02).half()
-    table = {(151936, 4096, 1): (2, 32), (151936, 4096, 4): (2, 32)}
-    for m in (1, 3):
+    table = {(151936, 4096, 1): (2, 32), (151936, 4096, 4): (2, 32), (151936, 4096, 8): (16, 32)}
+    for m in (1, 3, 5, 8):  # M = 5, 8: the matrix-core form
         x = torch.randn(m, 4096, device=dev, generator=g).half()
         y = gemv16.linear(x, w, table)
         ref = x.float() @ w.float().T
