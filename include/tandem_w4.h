@@ -129,6 +129,19 @@ int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
             const uint16_t* zeros, uint16_t* y, int M, int N, int K,
             int warps_k, int unroll, int ntile, int act, void* stream);
 
+/* tw4_mma with K split over `splits` workgroups per row-tile group, M <= 16, 2 <= splits <=
+ * min(16, K / 128): a workgroup covers 1 / splits of the quant groups, with x in LDS over that
+ * range only, and the last arriver of a tile group adds the splits partial sums in split order
+ * (deterministic) and writes y. ws / locks: tw4_gemm's caller-owned fp32 workspace (at least
+ * ceil(ceil(N / 16) / ntile) x splits x ntile x 256 floats) and int32 counters (one per tile group),
+ * zero before the first call and returned to zero by every call; calls that share them must not
+ * overlap. No counterpart in the reference: it extends w4_mma (csrc/w4_gemv.cu:619-648) for M = 4 .. 16
+ * with a large K, where each workgroup would otherwise read all of x from L2. */
+int tw4_mma_splitk(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+                   const uint16_t* zeros, uint16_t* y, float* ws, int32_t* locks,
+                   int64_t ws_floats, int64_t n_locks, int M, int N, int K,
+                   int warps_k, int unroll, int ntile, int splits, int act, void* stream);
+
 /* Fused-dequant GEMM for M > 16 (any M >= 1 works): x tiles double-buffered through LDS,
  * weights dequantized in registers into MFMA fragments, fp32 accumulation, optional split-K
  * across workgroups with a deterministic last-arriver reduction.

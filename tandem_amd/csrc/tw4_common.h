@@ -210,6 +210,101 @@ __host__ __device__ __forceinline__ int interleaved_dest_row(int src, int n) {
     return 16 * (rem >> 3) + 8 * h + (rem & 7);
 }
 
+// The end of a work unit, run by every thread of the workgroup. Wavefronts with `holder` set hold
+// the unit's fp32 tiles (rows 16 (wt0 + t) .., tokens m0 + 16 b ..) in acc. nsplit > 1: each stores
+// its partial to split slot su of ws; one agent-scope counter per split tile (st) tells the last
+// arriver, which adds the nsplit partials of the tile in split order (the result does not depend
+// on arrival order), returns the counter to zero for the next call and writes y. Partials and their
+// reads are agent-scope relaxed atomics (global_store / global_load sc1: coherent across the
+// XCDs' L2s without a cache-wide write-back or invalidate); each wavefront partial is stored
+// [fragment][component][lane], so every instruction moves 256 contiguous bytes. s_waitcnt vmcnt(0)
+// + barrier order the stores before the count. act = 1: SwiGLU epilogue (gate rows 4 kb + i and
+// up rows 8 + 4 kb + i sit in lanes l and l + 32).
+template <int MT, int NT, int WN>
+__device__ __forceinline__ void finish_unit(f4 (&acc)[NT][MT], bool holder, int wn, int lane, int tid, int nsplit,
+                                            int st, int su, float* __restrict__ ws, int* __restrict__ locks,
+                                            int& last_flag, h1* __restrict__ y, int M, int N, int m0, int wt0,
+                                            int tiles_n, int act) {
+    const int r = lane & 15, kb = lane >> 4;
+    if (nsplit > 1) {
+        constexpr int V = NT * MT * 4 * 64;  // floats per wavefront partial
+        if (holder) {
+            float* mine = ws + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        __hip_atomic_store(mine + ((t * MT + b) * 4 + c) * 64, acc[t][b][c], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(locks + st, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = old == nsplit - 1;
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        if (holder) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int v = 0; v < nsplit; ++v) {
+                const float* other = ws + ((static_cast<int64_t>(st) * nsplit + v) * WN + wn) * V + lane;
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int b = 0; b < MT; ++b)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            acc[t][b][c] += __hip_atomic_load(other + ((t * MT + b) * 4 + c) * 64, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!holder) return;
+
+    if (act) {  // N % 16 == 0 (checked on the host)
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = wt0 + t;
+#pragma unroll
+            for (int b = 0; b < MT; ++b) {
+                f4 up;
+                up.x = lane_xor32(acc[t][b].x, lane);
+                up.y = lane_xor32(acc[t][b].y, lane);
+                up.z = lane_xor32(acc[t][b].z, lane);
+                up.w = lane_xor32(acc[t][b].w, lane);
+                const int m = m0 + 16 * b + r;
+                if (kb >= 2 || m >= M || tt >= tiles_n) continue;
+                const f4 g = acc[t][b];
+                const h4 o = h4{static_cast<h1>(silu(g.x) * up.x), static_cast<h1>(silu(g.y) * up.y),
+                                static_cast<h1>(silu(g.z) * up.z), static_cast<h1>(silu(g.w) * up.w)};
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + 8 * tt + 4 * kb) = o;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = 16 * (wt0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+        if (n >= N) continue;
+#pragma unroll
+        for (int b = 0; b < MT; ++b) {
+            const int m = m0 + 16 * b + r;
+            if (m >= M) continue;
+            const f4 a = acc[t][b];
+            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                h4{static_cast<h1>(a.x), static_cast<h1>(a.y), static_cast<h1>(a.z), static_cast<h1>(a.w)};
+        }
+    }
+}
+
 }  // namespace tw4
 
 // ------------------------------------------------------------------------------- host plumbing

@@ -751,7 +751,7 @@ template <bool PF, int XM, int U, int NT, int MT>
 __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
                                           const uint16_t* s16, const uint16_t* z16, const u4* smem, const DecodeLds& l,
                                           const h8* const (&xl)[MT], int xrow, f4 (&acc)[NT][MT], int g0, int ge,
-                                          int kb, uint32_t magic) {
+                                          int glo, int kb, uint32_t magic) {
     h8 xb[XM == kXGlobal ? U : 1][4][MT];
     if constexpr (XM == kXGlobal) {  // issued first: waiting for x never waits for the prefetch below
 #pragma unroll
@@ -783,7 +783,7 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
 #pragma unroll
             for (int b = 0; b < MT; ++b) {
                 if constexpr (XM != kXGlobal)
-                    xv[b] = bitcast<h8>(smem[xrow * l.xs + 16 * g + 4 * kb + s]);
+                    xv[b] = bitcast<h8>(smem[xrow * l.xs + 16 * (g - glo) + 4 * kb + s]);
                 else
                     xv[b] = xb[u][s][b];
             }
@@ -797,14 +797,20 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
     }
 }
 
-template <int WK, int U, int NT, int MT, int XM, bool NORM = false>
+// splits > 1: workgroup (tile group tg, split s) covers quant groups [s G / splits, (s + 1) G / splits)
+// only, with x in LDS over that range alone, and the splits partial sums of a tile group are added by
+// the last arriver (finish_unit: ws / locks, the GEMM's counter protocol).
+template <int WK, int U, int NT, int MT, int XM, bool NORM = false, bool SPLIT = false>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                     h1* __restrict__ y, int M, int N, int K, int act, NormIn nin) {
+                                                     h1* __restrict__ y, int M, int N, int K, int act, NormIn nin,
+                                                     float* __restrict__ ws, int* __restrict__ locks, int nsplit) {
     constexpr bool XLDS = XM != kXGlobal;
     constexpr int XB = XM == kXLdsWide ? 8 : 2;
     static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
     static_assert(!NORM || XLDS, "the fused norm stages x in LDS");
+    static_assert(!SPLIT || (MT == 1 && !NORM), "split-K: one batch tile, no fused norm");
+    const int splits = SPLIT ? nsplit : 1;  // a constant 1 where split-K is not compiled in
     if constexpr (U * MT > 4 && MT > 1) {
         return;  // register budget: never launched (tw4_mma rejects U * MT > 4 for M > 16)
     } else {
@@ -812,8 +818,10 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int tile0 = xcd_rotated_block() * NT;
-    const DecodeLds l = decode_lds(XLDS, M, K, 0, (WK - 1) * NT * MT * 64, NORM);
+    const int unit = xcd_rotated_block(), tg = unit / splits, split = unit - tg * splits;
+    const int tile0 = tg * NT;
+    const int glo = split * G / splits, R = (split + 1) * G / splits - glo;  // this workgroup's quant groups
+    const DecodeLds l = decode_lds(XLDS, M, 128 * R, 0, (WK - 1) * NT * MT * 64, NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
@@ -823,13 +831,13 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
 #pragma unroll
     for (int b = 0; b < MT; ++b)
         xl[b] = reinterpret_cast<const h8*>(x + static_cast<int64_t>(min(16 * b + r, M - 1)) * K + 32 * kb);
-    const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
+    const int gw = (R + WK - 1) / WK, gb = glo + min(wave * gw, R), ge = glo + min(wave * gw + gw, R);
     const int nch = (ge - gb + U - 1) / U;
 
     WeightSet<U, NT> a, b;
     const int kx = K >> 3;
-    const u4* xg = reinterpret_cast<const u4*>(x);
-    const XSlice xsl = x_slice(gb, ge, M);
+    const u4* xg = reinterpret_cast<const u4*>(x) + 16 * glo;  // the LDS image starts at group glo
+    const XSlice xsl = x_slice(gb - glo, ge - glo, M);
     if constexpr (XLDS) {
         if constexpr (NORM) {  // no branch around these loads (see stage_x_norm)
             u4 fx[kXB], fr[kXB], fw[kXB];
@@ -858,14 +866,14 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
     for (; i + 2 < nch; i += 2) {
-        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<true, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, glo, kb, magic);
     }
     if (i + 2 == nch) {
-        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
-        mma_chunk<false, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
+        mma_chunk<false, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, glo, kb, magic);
     } else if (i + 1 == nch) {
-        mma_chunk<false, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, kb, magic);
+        mma_chunk<false, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
     }
     if constexpr (NORM) write_residual<false>(xg, nin, kx, xsl, lane);
     if (WK > 1) {
@@ -877,13 +885,21 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
                 for (int bb = 0; bb < MT; ++bb) red[(((wave - 1) * NT + t) * MT + bb) * 64 + lane] = acc[t][bb];
         }
         __syncthreads();
-        if (wave != 0) return;
+        if (wave != 0 && splits == 1) return;
+        if (wave == 0) {
 #pragma unroll
-        for (int v = 0; v < WK - 1; ++v)
+            for (int v = 0; v < WK - 1; ++v)
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+                for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int bb = 0; bb < MT; ++bb) acc[t][bb] += red[((v * NT + t) * MT + bb) * 64 + lane];
+                    for (int bb = 0; bb < MT; ++bb) acc[t][bb] += red[((v * NT + t) * MT + bb) * 64 + lane];
+        }
+    }
+    if constexpr (SPLIT) {  // every thread takes part (the epilogue has workgroup barriers)
+        int* last_flag = reinterpret_cast<int*>(smem + l.total);  // one u4 past the layout
+        finish_unit<MT, NT, 1>(acc, wave == 0, 0, lane, threadIdx.x, splits, tg, unit, ws, locks, *last_flag, y, M, N,
+                               0, tile0, tiles, act);
+        return;
     }
     if (act) {  // N % 16 == 0 (checked on the host)
         const int half_n = N >> 1;
@@ -964,6 +980,9 @@ int decode_prepare(int dev) {
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds, true>);   \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLdsWide>);     \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXGlobal>);      \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds, false, true>);     \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLdsWide, false, true>); \
+    if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXGlobal, false, true>);  \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, kXGlobal>);      \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, kXGlobal>);
     TW4_DECODE_CONFIGS(TW4_ATTR)
@@ -1098,36 +1117,66 @@ extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t
 
 namespace tw4 {
 
-// One mma launch; nin (not null): the fused norm prologue, which needs x in LDS.
+// One mma launch; nin (not null): the fused norm prologue, which needs x in LDS. splits > 1: split-K
+// over workgroups (ws / locks: the partial sums and counters, zero before the first call).
 int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, int M, int N, int K, int warps_k,
-               int unroll, int ntile, int act, const NormIn* nin, hipStream_t st) {
+               int unroll, int ntile, int act, const NormIn* nin, float* ws, int* locks, int64_t ws_floats,
+               int64_t n_locks, int splits, hipStream_t st) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
     TW4_REQUIRE(mt == 1 || unroll * mt <= 4, TW4_ECONFIG,
                 "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
-    const int tiles = (N + 15) >> 4;
-    const bool xlds = mt == 1 && static_cast<size_t>(M) * ((K >> 3) + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
-    const int gw = ((K >> 7) + warps_k - 1) / max(warps_k, 1);
+    const int G = K >> 7, tiles = (N + 15) >> 4;
+    TW4_REQUIRE(splits >= 1 && splits <= 16 && splits <= G, TW4_EINVAL,
+                "mma: splits in 1 .. min(16, K / 128) (splits = %d, K = %d)", splits, K);
+    TW4_REQUIRE(splits == 1 || !nin, TW4_EINVAL, "mma: the fused norm needs whole rows (splits = 1)");
+    TW4_REQUIRE(splits == 1 || mt == 1, TW4_EINVAL, "mma: split-K for M <= 16 only (M = %d)", M);
+    const int R = (G + splits - 1) / splits;  // the most quant groups a workgroup covers
+    const bool xlds = mt == 1 && static_cast<size_t>(M) * (16 * R + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+    const int gw = (R + warps_k - 1) / max(warps_k, 1);
     const bool wide = M * gw > 8;  // a lane's share of the staged slice, M gw / 4 chunks, is more than 2
     TW4_REQUIRE(!nin || xlds, TW4_ECONFIG,
                 "mma: the fused norm stages x in LDS: M (K + 8) 2 bytes <= %d (M = %d, K = %d)", kXLdsLimit, M, K);
     const NormIn none{nullptr, nullptr, nullptr, 0.0f};
+    const int64_t groups = (tiles + ntile - 1) / max(ntile, 1);
+    if (splits > 1) {
+        TW4_REQUIRE(ws && locks, TW4_EINVAL, "mma: split-K needs a workspace and counters");
+        TW4_REQUIRE(groups * splits * ntile * mt * 256 <= ws_floats && groups <= n_locks, TW4_ESPACE,
+                    "mma: split-K workspace too small for %lld tile groups x %d splits", static_cast<long long>(groups),
+                    splits);
+    }
 #define TW4_MMA_CASE(WK, U, T)                                                                                 \
     if (warps_k == WK && unroll == U && ntile == T) {                                                          \
-        const size_t lds =                                                                                     \
-            16 * static_cast<size_t>(decode_lds(xlds, M, K, 0, (WK - 1) * T * mt * 64, nin != nullptr).total); \
-        const unsigned grid = (tiles + T - 1) / T;                                                             \
-        if (nin)                                                                                               \
-            mma_kernel<WK, U, T, 1, kXLds, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin); \
+        const size_t lds = 16 * (static_cast<size_t>(                                                          \
+                                     decode_lds(xlds, M, 128 * R, 0, (WK - 1) * T * mt * 64, nin != nullptr).total) + \
+                                 1); /* + the split-K flag */                                                  \
+        const unsigned grid = static_cast<unsigned>(groups * splits);                                         \
+        if (splits > 1 && xlds && wide)                                                                        \
+            mma_kernel<WK, U, T, 1, kXLdsWide, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, \
+                                                                                      act, none, ws, locks, splits); \
+        else if (splits > 1 && xlds)                                                                           \
+            mma_kernel<WK, U, T, 1, kXLds, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, \
+                                                                                  none, ws, locks, splits);    \
+        else if (splits > 1)                                                                                   \
+            mma_kernel<WK, U, T, 1, kXGlobal, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, \
+                                                                                     act, none, ws, locks, splits); \
+        else if (nin)                                                                                          \
+            mma_kernel<WK, U, T, 1, kXLds, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin, \
+                                                                             ws, locks, splits);               \
         else if (xlds && wide)                                                                                 \
-            mma_kernel<WK, U, T, 1, kXLdsWide><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 1, kXLdsWide><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none, \
+                                                                          ws, locks, splits);                  \
         else if (xlds)                                                                                         \
-            mma_kernel<WK, U, T, 1, kXLds><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 1, kXLds><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none, ws, \
+                                                                      locks, splits);                          \
         else if (mt == 1)                                                                                      \
-            mma_kernel<WK, U, T, 1, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 1, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
+                                                                         ws, locks, splits);                   \
         else if (mt == 2)                                                                                      \
-            mma_kernel<WK, U, T, 2, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 2, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
+                                                                         ws, locks, splits);                   \
         else                                                                                                   \
-            mma_kernel<WK, U, T, 4, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none); \
+            mma_kernel<WK, U, T, 4, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
+                                                                         ws, locks, splits);                   \
         TW4_LAUNCH_CHECK("mma: launch");                                                                       \
         return TW4_OK;                                                                                         \
     }
@@ -1150,7 +1199,29 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
     if (rc) return rc;
     return mma_launch(reinterpret_cast<const h1*>(x), reinterpret_cast<const u4*>(packed),
                       reinterpret_cast<const h1*>(scales), reinterpret_cast<const h1*>(zeros), reinterpret_cast<h1*>(y),
-                      M, N, K, warps_k, unroll, ntile, act, nullptr, static_cast<hipStream_t>(stream));
+                      M, N, K, warps_k, unroll, ntile, act, nullptr, nullptr, nullptr, 0, 0, 1,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw4_mma_splitk(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                              uint16_t* y, float* ws, int32_t* locks, int64_t ws_floats, int64_t n_locks, int M, int N,
+                              int K, int warps_k, int unroll, int ntile, int splits, int act, void* stream) {
+    int rc = check_operands("mma", x, packed, scales, zeros, y, M, N, K);
+    if (rc) return rc;
+    TW4_REQUIRE(M >= 1 && M <= 64, TW4_EINVAL, "mma: 1 <= M <= 64 (M = %d)", M);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "mma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    TW4_REQUIRE(ws_floats >= 0 && n_locks >= 0, TW4_EINVAL, "mma: workspace sizes must be >= 0");
+    TW4_REQUIRE(splits >= 1 && splits <= 16 && splits <= K / 128, TW4_EINVAL,
+                "mma: splits in 1 .. min(16, K / 128) (splits = %d, K = %d)", splits, K);
+    TW4_REQUIRE(splits == 1 || M <= 16, TW4_EINVAL, "mma: split-K for M <= 16 only (M = %d)", M);
+    TW4_REQUIRE(splits == 1 || (ws && locks), TW4_EINVAL, "mma: split-K needs a workspace and counters");
+    rc = ensure_prepared();
+    if (rc) return rc;
+    return mma_launch(reinterpret_cast<const h1*>(x), reinterpret_cast<const u4*>(packed),
+                      reinterpret_cast<const h1*>(scales), reinterpret_cast<const h1*>(zeros), reinterpret_cast<h1*>(y),
+                      M, N, K, warps_k, unroll, ntile, act, nullptr, ws, reinterpret_cast<int*>(locks), ws_floats,
+                      n_locks, splits, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint16_t* residual_out,
@@ -1182,7 +1253,8 @@ extern "C" int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint
     auto zp = reinterpret_cast<const h1*>(zeros);
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
-    if (kind == 1) return mma_launch(xp, wp, sp, zp, yp, M, N, K, warps_k, unroll, ntile, act, &nin, st);
+    if (kind == 1) return mma_launch(xp, wp, sp, zp, yp, M, N, K, warps_k, unroll, ntile, act, &nin, nullptr, nullptr, 0, 0, 1,
+                                     st);
     switch (M) {
         case 1: return gemv_dispatch<1, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);
         case 2: return gemv_dispatch<2, true>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, nin, st);

@@ -142,6 +142,9 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 #   ("gemvm", warps_k, unroll, ntile)  the GEMV's arithmetic (exact q - z, scale per group) on the
 #                                      matrix cores, M <= 4
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
+#   ("mmak", warps_k, unroll, ntile, splits)   the same with K split over `splits` workgroups per
+#                                      row-tile group (x in LDS over 1 / splits of K; the last arriver
+#                                      adds the partials, w4_gemm's workspace), M <= 16
 #   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
 # iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
@@ -333,6 +336,10 @@ class W4Linear(nn.Module):
                     return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
                 if kind == "gemvm" and m <= 4:  # the GEMV's arithmetic on the matrix cores
                     return ext.w4_gemv_mfma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
+                if kind == "mmak":  # the matrix-core decode kernel with K split over workgroups
+                    buf, locks = w4_hip.workspace(x.device)
+                    return ext.w4_mma_splitk(x, self.packed, self.scales, self.zeros, buf, locks, *cfg,
+                                             int(self.silu_mul))
                 if kind != "mma":  # gemv / gemvm past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))

@@ -46,6 +46,7 @@ _SIGNATURES = {
     "tw4_gemv_act": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_mfma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tw4_mma_splitk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
@@ -212,6 +213,27 @@ class W4Extension:
         with torch.cuda.device(x.device):
             check(self.lib.tw4_mma(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
                                    int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
+        return y
+
+    def w4_mma_splitk(self, x, w, s, z, ws, locks, warps_k: int, unroll: int, ntile: int, splits: int,
+                      act: int) -> torch.Tensor:
+        """w4_mma with K split over `splits` workgroups per row-tile group (M <= 16): each covers
+        1 / splits of the quant groups with x in LDS over that range; the last arriver adds the
+        partial sums in split order (ws / locks: w4_gemm's workspace)."""
+        m, n, k = check_operands("w4_mma", x, w, s, z)
+        if not 1 <= m <= 16:
+            raise RuntimeError("w4_mma_splitk: M <= 16 (one 16-token batch tile)")
+        if not (ws.is_cuda and ws.dtype == torch.float32 and locks.is_cuda and locks.dtype == torch.int32
+                and ws.device == x.device and locks.device == x.device and ws.is_contiguous()
+                and locks.is_contiguous()):
+            raise RuntimeError("w4_mma_splitk: float32 workspace and int32 locks (zero) on x's GPU")
+        if act not in (0, 1) or (act and n % 16):
+            raise RuntimeError("w4_mma: act 0, or 1 (SwiGLU) with N % 16 == 0")
+        y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
+        with torch.cuda.device(x.device):
+            check(self.lib.tw4_mma_splitk(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), _ptr(ws), _ptr(locks),
+                                          ws.numel(), locks.numel(), m, n, k, int(warps_k), int(unroll), int(ntile),
+                                          int(splits), int(act), _stream(x)))
         return y
 
     def w4_gemm(self, x, w, s, z, ws, locks, mt: int, nt: int, warps_n: int, warps_k: int, stages: int,

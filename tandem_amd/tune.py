@@ -95,7 +95,7 @@ def main(argv=None) -> int:
     ap.add_argument("--model", default="qwen3-8b", choices=sorted(MODELS))
     ap.add_argument("--projs", default="", help="comma list of projections (default: all)")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--kinds", default="gemv,mma", help="gemv, mma, gemm, dense")
+    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, mma, mmak, gemm, dense")
     ap.add_argument("--splits", default="0,1,2,4,8")
     ap.add_argument("--act", action="store_true", help="time the SwiGLU epilogue (gate_up only)")
     ap.add_argument("--footprint-mb", type=float, default=1024.0)
@@ -164,6 +164,17 @@ def main(argv=None) -> int:
                     except RuntimeError:  # unroll * batch tiles above 4
                         continue
                     res[("mma", *cfg)] = us
+            if "mmak" in kinds and m <= 16:
+                for cfg in w4_hip.decode_configs():
+                    for sp in (int(v) for v in a.splits.split(",")):
+                        if sp < 2 or sp > k // 128:
+                            continue
+                        try:
+                            us = time_us([lambda w=w, c=cfg, s=sp: ext.w4_mma_splitk(x, *w, buf, locks, *c, s, act)
+                                          for w in ws], stream)
+                        except RuntimeError:
+                            continue
+                        res[("mmak", *cfg, sp)] = us
             if "gemm" in kinds:
                 g = k // 128
                 for cfg in w4_hip.gemm_configs():

@@ -269,6 +269,58 @@ def test_mma_silu_mul(ext):
                 check_close(y, ref, 0.02, 0.01, (k, n, m, cfg))
 
 
+def test_mma_split_k_every_config(ext):
+    """The matrix-core decode kernel with K split over workgroups (tw4_mma_splitk): M = 1 .. 16,
+    every compiled config, 2 .. 8 splits (uneven group ranges included), plain and SwiGLU; the
+    counters are back at zero after each call."""
+    buf, locks = w4_hip.workspace(DEV)
+    ran = 0
+    for k, n, interleave in ((256, 520, False), (1024, 64, False), (4096, 1000, False), (12288, 256, False),
+                             (1024, 512, True)):
+        c = Case(k, n, seed=21, interleave=interleave)
+        g = k // 128
+        for m in (1, 3, 8, 13, 16):
+            x = c.x(m, seed=800 + m)
+            ref = o.swiglu_reference(x, c.w_exact) if interleave else o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                for splits in (2, 3, 8):
+                    if splits > g:
+                        continue
+                    y = ext.w4_mma_splitk(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, int(interleave))
+                    ran += 1
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits, interleave))
+    torch.cuda.synchronize()
+    assert int(locks.abs().sum()) == 0
+    assert ran > 3 * len(DECODE_CONFIGS)
+
+
+def test_mma_split_k_deterministic_and_graph_replay(ext):
+    """Split-K decode: identical bits on every call (the partials are added in split order), and
+    correct on every replay of a captured graph with eager work in between."""
+    buf, locks = w4_hip.workspace(DEV)
+    c = Case(12288, 512, seed=22)
+    x = gpu(c.x(8, seed=23))
+    cfg = (4, 2, 1, 4)
+    first = ext.w4_mma_splitk(x, c.packed, c.s, c.zz, buf, locks, *cfg, 0)
+    for _ in range(4):
+        assert torch.equal(ext.w4_mma_splitk(x, c.packed, c.s, c.zz, buf, locks, *cfg, 0), first)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = ext.w4_mma_splitk(x, c.packed, c.s, c.zz, buf, locks, *cfg, 0)
+    rng = np.random.default_rng(24)
+    for _ in range(3):
+        xn = rng.standard_normal((8, 12288)).astype(np.float16)
+        x.copy_(gpu(xn))
+        graph.replay()
+        torch.cuda.synchronize()
+        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "split-K replay")
+        check_close(ext.w4_mma_splitk(x, c.packed, c.s, c.zz, buf, locks, *cfg, 0), o.linear(xn, c.w_exact),
+                    0.02, 0.01, "split-K eager")
+    assert int(locks.abs().sum()) == 0
+
+
 def test_gemm_every_config(ext):
     """GEMM: every compiled config, partial token and row tiles, split-K of every tile or of the last
     wave only (stages 0, the resident-x variant: the fewest splits that fit, chosen on the host); the

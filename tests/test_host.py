@@ -83,6 +83,14 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_add_rms_norm(_fake(4104), _fake(), _fake(), 1, 1024, 1e-6, None), "aligned"),
         (lambda: lib.tw4_add_rms_norm(_fake(), None, _fake(), 1, 1024, 1e-6, None), "null"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 4, 24, 128, 4, 2, 1, 1, None), "SwiGLU"),
+        (lambda: lib.tw4_mma_splitk(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
+                                    8, 64, 1024, 4, 2, 1, 17, 0, None), "splits"),
+        (lambda: lib.tw4_mma_splitk(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
+                                    8, 64, 256, 4, 2, 1, 3, 0, None), "splits"),
+        (lambda: lib.tw4_mma_splitk(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
+                                    17, 64, 1024, 4, 2, 1, 2, 0, None), "M <= 16"),
+        (lambda: lib.tw4_mma_splitk(_fake(), _fake(), _fake(), _fake(), _fake(), None, _fake(), 1 << 20, 1024,
+                                    8, 64, 1024, 4, 2, 1, 2, 0, None), "workspace"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
                               32, 64, 128, 2, 1, 4, 1, 2, 17, 0, None), "splits"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
@@ -212,6 +220,8 @@ def test_tables_are_well_formed():
             assert 1 <= m <= 16 and k % 128 == 0 and n % 8 == 0
             if cfg[0] == "gemm":  # a compiled GEMM config and a split mode
                 assert len(cfg) == 7 and tuple(cfg[1:6]) in gemm and 0 <= cfg[6] <= 16
+            elif cfg[0] == "mmak":  # a compiled decode config and 2 .. 16 K splits (at most one per group)
+                assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 2 <= cfg[4] <= min(16, k // 128)
             else:  # a compiled decode config; gemv / gemvm only where they run (M <= 4)
                 assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
                 assert cfg[0] == "mma" or m <= 4
