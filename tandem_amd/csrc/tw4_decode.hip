@@ -28,7 +28,9 @@
 //         operands, so each MFMA sums 32 distinct k of the group. B columns r >= M read row
 //         M - 1: they only feed D columns that are never stored. D holds output rows 4 kb + i
 //         (i = 0..3) of batch column r in lane (kb, r). x comes from LDS when M (K + 8) 2 bytes
-//         fit in 80 KB, else straight from global memory (issued before the prefetch).
+//         fit in 80 KB, else straight from global memory (issued before the prefetch). Split-K
+//         form (M <= 16): each workgroup covers 1 / splits of the quant groups, so only that part
+//         of x has to fit in LDS, and the last arriver of a row-tile group adds the partial sums.
 //   act = 1: rows are in interleave_gate_up order (gate rows 0..7 of a tile, then its up rows).
 //         mma: the gate rows 4 kb + i (kb = 0, 1) and up rows 8 + 4 kb + i of a feature sit in
 //         lanes l and l + 32; gemv: in lanes i and i + 8. One cross-lane exchange pairs them and
