@@ -950,7 +950,9 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
 constexpr int kMaxDevices = 64;
 constexpr int kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr int kXLdsLimit = 80 * 1024;    // mma keeps x in LDS up to this size (M = 8 at K = 4096)
+constexpr int kXLdsBig = 136 * 1024;     // ... and up to this one when the grid has at most one workgroup per CU
 static int g_decode_ready[kMaxDevices];
+static int g_decode_cus[kMaxDevices];
 
 template <typename Kern>
 int allow_lds(Kern kern) {
@@ -965,6 +967,10 @@ int decode_prepare(int dev) {
         return TW4_EINVAL;
     }
     if (g_decode_ready[dev]) return TW4_OK;
+    int cus = 0;
+    hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return tw4host::hip_fail(e, "init: multiprocessor count");
+    g_decode_cus[dev] = cus;
     int rc = TW4_OK;
 #define TW4_ATTR_GEMV(WK, U, T, NORM)                                        \
     if (rc == TW4_OK) rc = allow_lds(gemv_kernel<1, WK, U, T, NORM>);        \
@@ -1133,13 +1139,18 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
     TW4_REQUIRE(splits == 1 || !nin, TW4_EINVAL, "mma: the fused norm needs whole rows (splits = 1)");
     TW4_REQUIRE(splits == 1 || mt == 1, TW4_EINVAL, "mma: split-K for M <= 16 only (M = %d)", M);
     const int R = (G + splits - 1) / splits;  // the most quant groups a workgroup covers
-    const bool xlds = mt == 1 && static_cast<size_t>(M) * (16 * R + 1) * 16 <= static_cast<size_t>(kXLdsLimit);
+    const size_t x_bytes = static_cast<size_t>(M) * (16 * R + 1) * 16;
+    const bool xlds_small = mt == 1 && x_bytes <= static_cast<size_t>(kXLdsLimit);
     const int gw = (R + warps_k - 1) / max(warps_k, 1);
     const bool wide = M * gw > 8;  // a lane's share of the staged slice, M gw / 4 chunks, is more than 2
-    TW4_REQUIRE(!nin || xlds, TW4_ECONFIG,
+    TW4_REQUIRE(!nin || xlds_small, TW4_ECONFIG,
                 "mma: the fused norm stages x in LDS: M (K + 8) 2 bytes <= %d (M = %d, K = %d)", kXLdsLimit, M, K);
     const NormIn none{nullptr, nullptr, nullptr, 0.0f};
     const int64_t groups = (tiles + ntile - 1) / max(ntile, 1);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+    // x in LDS past kXLdsLimit (one workgroup per CU) only where the grid fits the CUs at once
+    const bool few = groups * splits <= g_decode_cus[dev];
     if (splits > 1) {
         TW4_REQUIRE(ws && locks, TW4_EINVAL, "mma: split-K needs a workspace and counters");
         TW4_REQUIRE(groups * splits * ntile * mt * 256 <= ws_floats && groups <= n_locks, TW4_ESPACE,
@@ -1148,8 +1159,12 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
     }
 #define TW4_MMA_CASE(WK, U, T)                                                                                 \
     if (warps_k == WK && unroll == U && ntile == T) {                                                          \
+        const int red_u4 = (WK - 1) * T * mt * 64;                                                             \
+        const bool xlds = xlds_small || (mt == 1 && few && x_bytes <= static_cast<size_t>(kXLdsBig) &&         \
+                                         16 * (static_cast<size_t>(decode_lds(true, M, 128 * R, 0, red_u4).total) + 1) <= \
+                                             static_cast<size_t>(kMaxLds));                                    \
         const size_t lds = 16 * (static_cast<size_t>(                                                          \
-                                     decode_lds(xlds, M, 128 * R, 0, (WK - 1) * T * mt * 64, nin != nullptr).total) + \
+                                     decode_lds(xlds, M, 128 * R, 0, red_u4, nin != nullptr).total) +          \
                                  1); /* + the split-K flag */                                                  \
         const unsigned grid = static_cast<unsigned>(groups * splits);                                         \
         if (splits > 1 && xlds && wide)                                                                        \
