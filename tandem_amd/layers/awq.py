@@ -148,6 +148,8 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 #   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
 # iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
+# Keys (N, K, M[, "silu"], "norm") name the GEMV configuration of the fused add + RMSNorm prologue
+# (forward_norm), timed on its own; the plain key's entry is used where there is none.
 # Tables are keyed by device name and by gfx architecture; finalize() tries the name it is given,
 # then the architecture of the layer's GPU. (Same dispatch structure as
 # python/tandem/layers/awq.py:136-160.)
@@ -283,6 +285,13 @@ class W4Linear(nn.Module):
         key = (self.out_features, self.in_features, m)
         return (self.kernels.get((*key, "silu")) if self.silu_mul else None) or self.kernels.get(key, DEFAULT_KERNEL)
 
+    def norm_entry(self, m: int) -> W4Kernel:
+        """The entry forward_norm uses: (N, K, M[, "silu"], "norm") where the fused-norm GEMV was
+        timed on its own (its best configuration differs from the plain GEMV's: qkv at M = 1 runs
+        5.2 us with (4, 4, 1) against 6.1 us with the plain table's (8, 2, 1)), else decode_entry."""
+        key = (self.out_features, self.in_features, m) + (("silu",) if self.silu_mul else ()) + ("norm",)
+        return self.kernels.get(key) or self.decode_entry(m)
+
     def forward_norm(self, x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
                      eps: float) -> tuple[torch.Tensor, torch.Tensor]:
         """self(rms_norm(x + residual) * norm_weight) and the new residual x + residual (x itself
@@ -304,7 +313,7 @@ class W4Linear(nn.Module):
         m = x.shape[0] if x.dim() == 2 else 0
         if (1 <= m <= 16 and not self.awq_layout and _hip_ok(x) and os.environ.get("TANDEM_W4_FUSE_NORM", "1") != "0"
                 and x.is_contiguous() and x.dtype == torch.float16):
-            kind, *cfg = self.decode_entry(m)
+            kind, *cfg = self.norm_entry(m)
             groups = self.in_features // self.group
             one_batch = m * 16 * -(-groups // cfg[0]) <= FUSED_NORM_CHUNKS
             if kind == "gemv" and m <= 4 and one_batch:

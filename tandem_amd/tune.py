@@ -95,7 +95,7 @@ def main(argv=None) -> int:
     ap.add_argument("--model", default="qwen3-8b", choices=sorted(MODELS))
     ap.add_argument("--projs", default="", help="comma list of projections (default: all)")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, mma, mmak, gemm, dense")
+    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, gemvn, mma, mmak, gemm, dense")
     ap.add_argument("--splits", default="0,1,2,4,8")
     ap.add_argument("--act", action="store_true", help="time the SwiGLU epilogue (gate_up only)")
     ap.add_argument("--footprint-mb", type=float, default=1024.0)
@@ -150,6 +150,16 @@ def main(argv=None) -> int:
                     except RuntimeError:
                         continue
                     res[("gemv", *cfg)] = us
+            if "gemvn" in kinds and m <= 4:  # the GEMV with the add + RMSNorm prologue (tw4_decode_norm)
+                r = torch.randn(m, k, device=dev, dtype=torch.float16)
+                nw = (torch.rand(k, device=dev) + 0.5).half()
+                for cfg in w4_hip.decode_configs():
+                    try:
+                        us = time_us([lambda w=w, c=cfg: ext.w4_decode_norm(x, r, nw, 1e-6, *w, 0, *c, act)
+                                      for w in ws], stream)
+                    except RuntimeError:
+                        continue
+                    res[("gemvn", *cfg)] = us
             if "gemvm" in kinds and m <= 4:
                 for cfg in w4_hip.decode_configs():
                     try:

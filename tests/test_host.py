@@ -215,7 +215,10 @@ def test_tables_are_well_formed():
     gemm = set(w4_hip.gemm_configs())
     for table in awq.W4_KERNELS.values():
         for key, cfg in table.items():
-            assert len(key) == 3 or (len(key) == 4 and key[3] == "silu")
+            assert key[3:] in ((), ("silu",), ("norm",), ("silu", "norm"))
+            if key[-1] == "norm":  # the fused add + RMSNorm GEMV (forward_norm): a GEMV config, M <= 4
+                assert cfg[0] == "gemv" and tuple(cfg[1:]) in decode and key[2] <= 4
+                continue
             n, k, m = key[:3]
             assert 1 <= m <= 16 and k % 128 == 0 and n % 8 == 0
             if cfg[0] == "gemm":  # a compiled GEMM config and a split mode
