@@ -236,6 +236,20 @@ def test_tables_are_well_formed():
                 (cfg[0] == "mma" and tuple(cfg[1:]) in decode and m_max <= 64 and cfg[2] * -(-m_max // 16) <= 4)
 
 
+def test_norm_entry_lookup():
+    """forward_norm takes the (N, K, M[, silu], norm) entry, else the plain decode entry."""
+    lin = awq.W4Linear(256, 64, 128)
+    lin.kernels = {(64, 256, 1): ("gemv", 8, 2, 1), (64, 256, 1, "norm"): ("gemv", 4, 4, 1),
+                   (64, 256, 2): ("mma", 4, 2, 1), (64, 256, 2, "silu"): ("gemv", 4, 2, 1),
+                   (64, 256, 2, "silu", "norm"): ("gemv", 4, 1, 1)}
+    assert lin.decode_entry(1) == ("gemv", 8, 2, 1) and lin.norm_entry(1) == ("gemv", 4, 4, 1)
+    assert lin.norm_entry(2) == ("mma", 4, 2, 1)  # no plain norm entry: the decode entry
+    assert lin.norm_entry(3) == awq.DEFAULT_KERNEL
+    lin.silu_mul = True
+    assert lin.decode_entry(2) == ("gemv", 4, 2, 1) and lin.norm_entry(2) == ("gemv", 4, 1, 1)
+    assert lin.norm_entry(1) == ("gemv", 8, 2, 1)  # the silu key has no norm entry at M = 1
+
+
 def test_make_linear_and_finalize_quantized():
     class Q:
         group_size = 128
