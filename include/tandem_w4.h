@@ -170,8 +170,9 @@ int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
 /* Dense fp16 GEMV for small batches: y [M, N] = x [M, K] @ w [N, K]^T (w row-major, nn.Linear
  * layout), 1 <= M <= 8, K in {512, 1024, 2048, 4096}, fp32 accumulation; x and w 16-byte aligned.
  * Config: rows_inflight rows per wavefront in flight (plus the next block prefetched), rows_per_wave
- * contiguous rows per wavefront; rows_inflight 16 selects the matrix-core form (16-row tiles on
- * v_mfma_f32_16x16x32_f16, rows_per_wave a multiple of 16), for M = 5 .. 8. For the fp16 lm_head of
+ * contiguous rows per wavefront; rows_inflight 16 or 32 selects the matrix-core form (16-row tiles on
+ * v_mfma_f32_16x16x32_f16 with one or two 128-k chunks per step in flight, rows_per_wave a multiple
+ * of 16), for M = 5 .. 8. For the fp16 lm_head of
  * a W4A16 model.
  * Replaces gemv / _gemv_kernel (python/tandem/layers/triton_gemv.py:26-61, 180-218). */
 int tw4_gemv_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K,

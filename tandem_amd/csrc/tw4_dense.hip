@@ -11,8 +11,9 @@
 // DPP (within rows of 16 lanes) and two permlane swaps, and lane 0 writes the RB x M results.
 //
 // For M = 5 .. 8 the v_dot2 form reads M x 16 bytes of x from LDS per 16 weight bytes, which makes
-// it LDS-bound; the matrix-core form (rows_inflight = 16) takes 16-row tiles of w as the A operand
-// of v_mfma_f32_16x16x32_f16 and x as B, so one 16-byte B fragment serves 16 rows.
+// it LDS-bound; the matrix-core form (rows_inflight = 16 or 32: one or two 128-k chunks per step in
+// flight) takes 16-row tiles of w as the A operand of v_mfma_f32_16x16x32_f16 and x as B, so one
+// 16-byte B fragment serves 16 rows.
 #include "tw4_common.h"
 
 namespace tw4 {
@@ -119,42 +120,51 @@ __global__ void __launch_bounds__(256) dense_gemv_kernel(const h1* __restrict__ 
 // all of K in chunks of 128 k. Lane (kb, r) loads, for word s = 0..3 of a chunk, the 16 bytes of
 // row r at k = 128 c + 8 (4 s + kb) .. + 7 (one instruction per s: 64 contiguous bytes per row), and
 // feeds them as A row r; the B fragment of token r is x at the same k from LDS, so each MFMA sums 32
-// distinct k of the chunk. The next chunk (possibly the next tile's first) is in flight in a second
-// register set while the current one is multiplied. D holds rows 4 kb + i of token r in lane (kb, r).
+// distinct k of the chunk. D chunks form a step: the next step's D chunks (possibly the next tile's
+// first) are in flight in a second register set while the current ones are multiplied, 4 D KB per
+// wavefront. D holds rows 4 kb + i of token r in lane (kb, r).
 // x: 8 token rows in LDS (rows past M repeat row M - 1; B columns r >= 8 read row 7 and feed D
 // columns that are never stored), row stride K / 8 + 1 chunks so the 16 rows of a fragment read hit
-// different banks. Staged once per workgroup, its loads issued before the first weight chunk.
+// different banks. Staged once per workgroup, its loads issued before the first weight chunks.
 constexpr int kMmaWaves = 8;  // wavefronts per workgroup of the matrix-core form (one x copy each)
 
+template <int D>
 struct ChunkSet {
-    u4 w[4];
+    u4 w[D][4];
 };
 
 // Plain (cached) loads: an instruction reads 64 bytes of each of 16 rows, half of a 128-byte line whose
 // other half the next word's load reads (with non-temporal loads the tile ran 2 % slower).
-__device__ __forceinline__ void load_chunk16(ChunkSet& cs, const u4* wrow, int c, int kb) {
+template <int D>
+__device__ __forceinline__ void load_chunks16(ChunkSet<D>& cs, const u4* wrow, int c, int kb) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) cs.w[s] = wrow[16 * c + 4 * s + kb];
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) cs.w[d][s] = wrow[16 * (c + d) + 4 * s + kb];
 }
 
-template <bool PF>
-__device__ __forceinline__ void mma16_step(const ChunkSet& cur, ChunkSet& nxt, const u4* nrow, int nc, const u4* xr,
-                                           int c, int kb, f4& acc) {
-    if constexpr (PF) load_chunk16(nxt, nrow, nc, kb);
+template <bool PF, int D>
+__device__ __forceinline__ void mma16_step(const ChunkSet<D>& cur, ChunkSet<D>& nxt, const u4* nrow, int nc,
+                                           const u4* xr, int c, int kb, f4& acc) {
+    if constexpr (PF) load_chunks16<D>(nxt, nrow, nc, kb);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch above the math
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-        acc = mfma16x16x32(bitcast<h8>(cur.w[s]), bitcast<h8>(xr[16 * c + 4 * s + kb]), acc);
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            acc = mfma16x16x32(bitcast<h8>(cur.w[d][s]), bitcast<h8>(xr[16 * (c + d) + 4 * s + kb]), acc);
 }
 
-// J = K / 512 x chunks per thread for the staging (K <= 4096: at most 8)
-template <int J>
+// J = K / 512 x chunks per thread for the staging (K <= 4096: at most 8); D = chunks per step, with
+// 2 D <= 4 J (the K / 128 chunks of a row are a whole, even number of steps).
+template <int J, int D>
 __global__ void __launch_bounds__(kMmaWaves * 64) dense_mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                                    h1* __restrict__ y, int Mx, int N,
                                                                    int rows_per_wave) {
     extern __shared__ u4 xs[];
     constexpr int kc = 64 * J;  // 16-byte chunks per row of x and w
-    constexpr int C = kc / 16;  // 128-k chunks per row (even)
+    constexpr int C = kc / 16;  // 128-k chunks per row
+    static_assert(C % (2 * D) == 0, "a row is an even number of D-chunk steps");
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, kb = lane >> 4;
     const int row0 = (blockIdx.x * kMmaWaves + wave) * rows_per_wave;
@@ -174,8 +184,8 @@ __global__ void __launch_bounds__(kMmaWaves * 64) dense_mma_kernel(const h1* __r
         xv[j] = xg[static_cast<int64_t>(min(m, Mx - 1)) * kc + (f - m * kc)];
     }
     __builtin_amdgcn_sched_barrier(0);
-    ChunkSet a, b;
-    load_chunk16(a, wrow(0), 0, kb);  // tiles == 0: a valid row, never used
+    ChunkSet<D> a, b;
+    load_chunks16<D>(a, wrow(0), 0, kb);  // tiles == 0: a valid row, never used
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -188,14 +198,14 @@ __global__ void __launch_bounds__(kMmaWaves * 64) dense_mma_kernel(const h1* __r
     const u4* xr = xs + min(r, 7) * (kc + 1);
     for (int t = 0; t < tiles; ++t) {
         const u4* cr = wrow(t);
-        const u4* nr = wrow(min(t + 1, last_tile));  // the last tile prefetches its own first chunk: unused
+        const u4* nr = wrow(min(t + 1, last_tile));  // the last tile prefetches its own first step: unused
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < C - 2; c += 2) {
-            mma16_step<true>(a, b, cr, c + 1, xr, c, kb, acc);
-            mma16_step<true>(b, a, cr, c + 2, xr, c + 1, kb, acc);
+        for (int c = 0; c < C - 2 * D; c += 2 * D) {
+            mma16_step<true, D>(a, b, cr, c + D, xr, c, kb, acc);
+            mma16_step<true, D>(b, a, cr, c + 2 * D, xr, c + D, kb, acc);
         }
-        mma16_step<true>(a, b, cr, C - 1, xr, C - 2, kb, acc);
-        mma16_step<true>(b, a, nr, 0, xr, C - 1, kb, acc);
+        mma16_step<true, D>(a, b, cr, C - D, xr, C - 2 * D, kb, acc);
+        mma16_step<true, D>(b, a, nr, 0, xr, C - D, kb, acc);
         const int n = row0 + 16 * t + 4 * kb;
         if (r < Mx && n < N) {
             h1* yp = y + static_cast<int64_t>(r) * N + n;
@@ -214,8 +224,10 @@ __global__ void __launch_bounds__(kMmaWaves * 64) dense_mma_kernel(const h1* __r
 
 // Compiled (rows in flight RB, rows per wavefront) configurations.
 #define TW4_DENSE_CONFIGS(X) X(1, 16) X(1, 32) X(2, 16) X(2, 32) X(2, 64) X(4, 32) X(4, 64)
-// Matrix-core form (rows_inflight 16): rows per wavefront, whole 16-row tiles.
-#define TW4_DENSE_MMA_CONFIGS(X) X(16, 16) X(16, 32) X(16, 64) X(16, 128)
+// Matrix-core form (rows_inflight 16 D: 16-row tiles, D chunks of 128 k per step in flight): rows
+// per wavefront, whole 16-row tiles.
+// (4 chunks per step ran 5-30 % slower on the Qwen3 lm_heads: no configuration compiled.)
+#define TW4_DENSE_MMA_CONFIGS(X) X(16, 16) X(16, 32) X(16, 64) X(16, 128) X(32, 16) X(32, 32)
 
 template <int M, int RB, int J>
 int dense_launch(const h1* x, const u4* w, h1* y, int Mx, int N, int rows_per_wave, hipStream_t st) {
@@ -240,22 +252,27 @@ int dense_by_k(const h1* x, const u4* w, h1* y, int Mx, int N, int K, int rows_p
     return TW4_EINVAL;
 }
 
-template <int J>
+template <int J, int D>
 int dense_mma_launch(const h1* x, const u4* w, h1* y, int Mx, int N, int rows_per_wave, hipStream_t st) {
     const int64_t waves = (static_cast<int64_t>(N) + rows_per_wave - 1) / rows_per_wave;
     const unsigned grid = static_cast<unsigned>((waves + kMmaWaves - 1) / kMmaWaves);
     const size_t lds = static_cast<size_t>(8) * (64 * J + 1) * 16;  // <= 65.7 KB
-    dense_mma_kernel<J><<<grid, kMmaWaves * 64, lds, st>>>(x, w, y, Mx, N, rows_per_wave);
+    dense_mma_kernel<J, D><<<grid, kMmaWaves * 64, lds, st>>>(x, w, y, Mx, N, rows_per_wave);
     TW4_LAUNCH_CHECK("gemv_f16: launch");
     return TW4_OK;
 }
 
+template <int D>
 int dense_mma(const h1* x, const u4* w, h1* y, int M, int N, int K, int rows_per_wave, hipStream_t st) {
+    if (K / 128 < 2 * D) {
+        tw4host::set_error("gemv_f16: rows in flight %d need K >= %d (K = %d)", 16 * D, 256 * D, K);
+        return TW4_ECONFIG;
+    }
     switch (K >> 9) {
-        case 1: return dense_mma_launch<1>(x, w, y, M, N, rows_per_wave, st);
-        case 2: return dense_mma_launch<2>(x, w, y, M, N, rows_per_wave, st);
-        case 4: return dense_mma_launch<4>(x, w, y, M, N, rows_per_wave, st);
-        case 8: return dense_mma_launch<8>(x, w, y, M, N, rows_per_wave, st);
+        case 1: if constexpr (D <= 2) return dense_mma_launch<1, D>(x, w, y, M, N, rows_per_wave, st); break;
+        case 2: return dense_mma_launch<2, D>(x, w, y, M, N, rows_per_wave, st);
+        case 4: return dense_mma_launch<4, D>(x, w, y, M, N, rows_per_wave, st);
+        case 8: return dense_mma_launch<8, D>(x, w, y, M, N, rows_per_wave, st);
         default: break;
     }
     tw4host::set_error("gemv_f16: K = %d (K in 512, 1024, 2048, 4096)", K);
@@ -293,7 +310,7 @@ extern "C" int tw4_gemv_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, i
     TW4_DENSE_CONFIGS(TW4_DENSE_CASE)
 #undef TW4_DENSE_CASE
 #define TW4_DENSE_MMA_CASE(RB, RPW) \
-    if (rows_inflight == RB && rows_per_wave == RPW) return dense_mma(xp, wp, yp, M, N, K, RPW, st);
+    if (rows_inflight == RB && rows_per_wave == RPW) return dense_mma<RB / 16>(xp, wp, yp, M, N, K, RPW, st);
     TW4_DENSE_MMA_CONFIGS(TW4_DENSE_MMA_CASE)
 #undef TW4_DENSE_MMA_CASE
     tw4host::set_error("gemv_f16: unsupported rows in flight / rows per wavefront %d / %d", rows_inflight,

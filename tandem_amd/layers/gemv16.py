@@ -6,8 +6,8 @@ functions, the same per-GPU ``CONFIGS`` keyed by (N, K, M bucket) and the same f
 ``F.linear`` (hipBLASLt here) for shapes without an entry. The kernel is tw4_gemv_f16 of
 libtandem_w4.so (hand-written HIP for gfx950, no Triton): it streams every row of w once with
 coalesced 16-byte loads and reduces on v_dot2_f32_f16, so it is bound by HBM bandwidth; for the
-M = 8 bucket a matrix-core form (config rows_inflight 16) multiplies 16-row tiles of w with x on
-v_mfma_f32_16x16x32_f16 instead, which reads x from LDS once per 16 rows rather than once per row.
+M = 8 bucket a matrix-core form (config rows_inflight 16 or 32) multiplies 16-row tiles of w with x
+on v_mfma_f32_16x16x32_f16 instead, which reads x from LDS once per 16 rows rather than once per row.
 
 The reference's fused norm / activation prologue (triton_gemv.py:92-178, 330-415) is not part of
 this build: it enabled no shape there (triton_gemv.py:316-329).
@@ -25,23 +25,26 @@ from torch import nn
 from tandem_amd.layers import w4_hip
 
 # Config per GPU and (N, K, M bucket): (rows_inflight, rows_per_wave) of tw4_gemv_f16 (rows_inflight
-# 16: the matrix-core form, rows_per_wave a multiple of 16), the fastest
-# of `python -m tandem_amd.tune --projs lm_head --kinds dense16,torch16` on the GPU. Shapes without
+# 16 / 32: the matrix-core form with one / two 128-k chunks per step in flight, rows_per_wave a
+# multiple of 16), the fastest of
+# `python -m tandem_amd.tune --projs lm_head --kinds dense16,torch16` on the GPU. Shapes without
 # an entry keep F.linear (python/tandem/layers/triton_gemv.py:221-268). Keyed by device name and by
 # gfx architecture.
 Config = tuple[int, int]
 GFX950_DENSE: dict[tuple[int, int, int], Config] = {
     # Qwen3-8B lm_head: 190 / 185 / 188 us at M = 1 / 2 / 4 (82-84 % of 8 TB/s) vs F.linear 243-251 us;
-    # M = 5 .. 8: the matrix-core form, 238-241 us vs F.linear 246-248 us (the v_dot2 form: 264-283 us)
+    # M = 5 .. 8: the matrix-core form with two chunks in flight, 231 us vs F.linear 246-249 us
+    # (one chunk: 234-239 us; the v_dot2 form: 270-283 us)
     (151936, 4096, 1): (4, 32),
     (151936, 4096, 2): (2, 32),
     (151936, 4096, 4): (2, 32),
-    (151936, 4096, 8): (16, 16),
-    # Qwen3-1.7B lm_head: 97-99 us at M = 1 .. 4, 121 us at M = 8 vs F.linear 203 us
+    (151936, 4096, 8): (32, 16),
+    # Qwen3-1.7B lm_head: 96-99 us at M = 1 .. 4, 119 us at M = 8 (the matrix-core form) vs
+    # F.linear 203 us
     (151936, 2048, 1): (2, 16),
     (151936, 2048, 2): (2, 16),
     (151936, 2048, 4): (2, 16),
-    (151936, 2048, 8): (2, 16),
+    (151936, 2048, 8): (16, 16),
 }
 CONFIGS: dict[str, dict[tuple[int, int, int], Config]] = {
     "AMD Instinct MI355X": GFX950_DENSE,
