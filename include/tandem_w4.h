@@ -142,6 +142,17 @@ int tw4_mma_splitk(const uint16_t* x, const int32_t* packed, const uint16_t* sca
                    int64_t ws_floats, int64_t n_locks, int M, int N, int K,
                    int warps_k, int unroll, int ntile, int splits, int act, void* stream);
 
+/* tw4_mma's persistent form, M <= 16, per_cu in 1 .. 8: at most per_cu workgroups per CU, each
+ * staging x (in LDS) once and streaming row-tile groups b, b + grid, ... with the next group's first
+ * chunk prefetched during the current group's last one; the same bits as tw4_mma with the same
+ * (warps_k, unroll, ntile). Needs M (K + 8) 2 bytes of x in LDS: up to 80 KB, or 136 KB where the grid
+ * has at most one workgroup per CU. No counterpart in the reference: it extends w4_mma
+ * (csrc/w4_gemv.cu:619-648) for the decode batches where staging x per workgroup costs more than
+ * the tile itself. */
+int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+                    const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+                    int warps_k, int unroll, int ntile, int per_cu, int act, void* stream);
+
 /* Fused-dequant GEMM for M > 16 (any M >= 1 works): x tiles double-buffered through LDS,
  * weights dequantized in registers into MFMA fragments, fp32 accumulation, optional split-K
  * across workgroups with a deterministic last-arriver reduction.

@@ -463,7 +463,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
-    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
+    TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
     const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
     const int nch = (ge - gb + U - 1) / U;
     float2* corr = reinterpret_cast<float2*>(smem + l.corr);
@@ -662,7 +662,7 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
-    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
+    TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
     const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
     const int nch = (ge - gb + U - 1) / U;
     float2* corr = reinterpret_cast<float2*>(smem + l.corr);
@@ -749,11 +749,14 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
 // slice is more than 2 chunks and the narrow one where the extra, repeated loads would cost.
 enum XMode { kXGlobal = 0, kXLds = 1, kXLdsWide = 2 };
 
-template <bool PF, int XM, int U, int NT, int MT>
-__device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& ts,
-                                          const uint16_t* s16, const uint16_t* z16, const u4* smem, const DecodeLds& l,
-                                          const h8* const (&xl)[MT], int xrow, f4 (&acc)[NT][MT], int g0, int ge,
-                                          int glo, int kb, uint32_t magic) {
+// PF: load the next chunk, groups pg .. pg + U - 1 of the streams pts (the next chunk of this tile, or
+// the first of the workgroup's next tile group), into nxt. FULL: all U groups of this chunk are in
+// range (every chunk but a tile's last).
+template <bool PF, int XM, int U, int NT, int MT, bool FULL = PF>
+__device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt, const TileStreams<NT>& pts,
+                                          int pg, const uint16_t* s16, const uint16_t* z16, const u4* smem,
+                                          const DecodeLds& l, const h8* const (&xl)[MT], int xrow, f4 (&acc)[NT][MT],
+                                          int g0, int ge, int glo, int kb, uint32_t magic) {
     h8 xb[XM == kXGlobal ? U : 1][4][MT];
     if constexpr (XM == kXGlobal) {  // issued first: waiting for x never waits for the prefetch below
 #pragma unroll
@@ -765,13 +768,13 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
                 for (int b = 0; b < MT; ++b) xb[u][s][b] = xl[b][16 * g + s];  // k = 128 g + 32 kb + 8 s .. + 7
         }
     }
-    if constexpr (PF) load_chunk<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1);
+    if constexpr (PF) load_chunk<U, NT>(nxt, pts, s16, z16, pg, ge - 1);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads above the math: the scheduler would sink them
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int graw = g0 + u;  // a chunk that prefetches is not the last: all its groups are in range
-        const bool valid = PF || graw < ge;
-        const int g = PF ? graw : min(graw, ge - 1);
+        const int graw = g0 + u;
+        const bool valid = FULL || graw < ge;
+        const int g = FULL ? graw : min(graw, ge - 1);
         GroupQ p[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -802,7 +805,10 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
 // splits > 1: workgroup (tile group tg, split s) covers quant groups [s G / splits, (s + 1) G / splits)
 // only, with x in LDS over that range alone, and the splits partial sums of a tile group are added by
 // the last arriver (finish_unit: ws / locks, the GEMM's counter protocol).
-template <int WK, int U, int NT, int MT, int XM, bool NORM = false, bool SPLIT = false>
+// PERSIST: a grid smaller than the tile groups; workgroup u takes tile groups u, u + gridDim.x, ...
+// with x staged once, each wavefront prefetching the next tile group's first chunk during its last
+// one. Two workgroup barriers per tile group guard the reduction buffer.
+template <int WK, int U, int NT, int MT, int XM, bool NORM = false, bool SPLIT = false, bool PERSIST = false>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                      h1* __restrict__ y, int M, int N, int K, int act, NormIn nin,
@@ -812,6 +818,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
     static_assert(!NORM || XLDS, "the fused norm stages x in LDS");
     static_assert(!SPLIT || (MT == 1 && !NORM), "split-K: one batch tile, no fused norm");
+    static_assert(!PERSIST || (XLDS && !NORM && !SPLIT), "persistent: x in LDS, no fused norm, no split-K");
     const int splits = SPLIT ? nsplit : 1;  // a constant 1 where split-K is not compiled in
     if constexpr (U * MT > 4 && MT > 1) {
         return;  // register budget: never launched (tw4_mma rejects U * MT > 4 for M > 16)
@@ -820,14 +827,15 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int unit = xcd_rotated_block(), tg = unit / splits, split = unit - tg * splits;
-    const int tile0 = tg * NT;
+    const int unit = xcd_rotated_block(), split = unit % splits;
+    int tg = unit / splits;
+    int tile0 = tg * NT;
     const int glo = split * G / splits, R = (split + 1) * G / splits - glo;  // this workgroup's quant groups
     const DecodeLds l = decode_lds(XLDS, M, 128 * R, 0, (WK - 1) * NT * MT * 64, NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
     const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
-    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
+    TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
     const int xrow = min(r, M - 1);  // B columns past M: any valid row, their D columns are not stored
     const h8* xl[MT];
 #pragma unroll
@@ -861,6 +869,23 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
     }
 
+    const int ngroups = (tiles + NT - 1) / NT;
+    for (int pass = 0;; ++pass) {  // one pass per tile group (PERSIST: several)
+    const int tg_next = tg + static_cast<int>(gridDim.x);
+    const bool more = PERSIST && tg_next < ngroups;  // uniform across the workgroup
+    // The streams the pass's last chunk prefetches from. Last pass: weight blocks of an empty buffer
+    // range (out-of-range buffer loads return zeros without a memory access) and the current tile
+    // group's group parameters, already cached.
+    TileStreams<NT> tsn = ts;
+    if constexpr (PERSIST) {
+        if (more) {
+            tsn = tile_streams<NT>(w, s16, z16, tg_next * NT, tiles, N, G, lane);
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                tsn.w[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<u4*>(w), 0, 0, kBufferFlags);
+        }
+    }
     f4 acc[NT][MT];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -868,18 +893,27 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
         for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
     for (; i + 2 < nch; i += 2) {
-        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
-        mma_chunk<true, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, glo, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge,
+                                       glo, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(b, a, ts, gb + U * (i + 2), s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1),
+                                       ge, glo, kb, magic);
     }
+    // A tile's last chunk. PERSIST: it prefetches the next tile group's first chunk, which the next
+    // pass finds in a (on the last pass: nothing from memory, see tsn).
     if (i + 2 == nch) {
-        mma_chunk<true, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
-        mma_chunk<false, XM, U, NT, MT>(b, a, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge, glo, kb, magic);
+        mma_chunk<true, XM, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge,
+                                       glo, kb, magic);
+        mma_chunk<PERSIST, XM, U, NT, MT, false>(b, a, tsn, gb, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge,
+                                                 glo, kb, magic);
     } else if (i + 1 == nch) {
-        mma_chunk<false, XM, U, NT, MT>(a, b, ts, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo, kb, magic);
+        mma_chunk<PERSIST, XM, U, NT, MT, false>(a, b, tsn, gb, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo,
+                                                 kb, magic);
+        if constexpr (PERSIST) a = b;
     }
     if constexpr (NORM) write_residual<false>(xg, nin, kx, xsl, lane);
     if (WK > 1) {
         f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][MT][64]
+        if (PERSIST && pass > 0) __syncthreads();  // wavefront 0 has read the previous tile group's sums
         if (wave > 0) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
@@ -887,7 +921,6 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
                 for (int bb = 0; bb < MT; ++bb) red[(((wave - 1) * NT + t) * MT + bb) * 64 + lane] = acc[t][bb];
         }
         __syncthreads();
-        if (wave != 0 && splits == 1) return;
         if (wave == 0) {
 #pragma unroll
             for (int v = 0; v < WK - 1; ++v)
@@ -903,7 +936,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
                                0, tile0, tiles, act);
         return;
     }
-    if (act) {  // N % 16 == 0 (checked on the host)
+    if (wave == 0 && act) {  // N % 16 == 0 (checked on the host)
         const int half_n = N >> 1;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -924,20 +957,25 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
                 *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + f) = o;
             }
         }
-        return;
-    }
+    } else if (wave == 0) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int n = 16 * (tile0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
-        if (n >= N) continue;
+        for (int t = 0; t < NT; ++t) {
+            const int n = 16 * (tile0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+            if (n >= N) continue;
 #pragma unroll
-        for (int bb = 0; bb < MT; ++bb) {
-            const int m = 16 * bb + r;
-            if (m >= M) continue;
-            const f4 a4 = acc[t][bb];
-            *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
-                h4{static_cast<h1>(a4.x), static_cast<h1>(a4.y), static_cast<h1>(a4.z), static_cast<h1>(a4.w)};
+            for (int bb = 0; bb < MT; ++bb) {
+                const int m = 16 * bb + r;
+                if (m >= M) continue;
+                const f4 a4 = acc[t][bb];
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                    h4{static_cast<h1>(a4.x), static_cast<h1>(a4.y), static_cast<h1>(a4.z), static_cast<h1>(a4.w)};
+            }
         }
+    }
+    if (!more) return;
+    ts = tsn;
+    tg = tg_next;
+    tile0 = tg * NT;
     }
     }
 }
@@ -1127,9 +1165,10 @@ namespace tw4 {
 
 // One mma launch; nin (not null): the fused norm prologue, which needs x in LDS. splits > 1: split-K
 // over workgroups (ws / locks: the partial sums and counters, zero before the first call).
+// per_cu > 0: the persistent form, at most per_cu workgroups per CU, each streaming several tile groups.
 int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, int M, int N, int K, int warps_k,
                int unroll, int ntile, int act, const NormIn* nin, float* ws, int* locks, int64_t ws_floats,
-               int64_t n_locks, int splits, hipStream_t st) {
+               int64_t n_locks, int splits, hipStream_t st, int per_cu = 0) {
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
     TW4_REQUIRE(mt == 1 || unroll * mt <= 4, TW4_ECONFIG,
                 "mma: M = %d takes %d batch tiles; unroll %d x %d tiles > 4 is not compiled", M, mt, unroll, mt);
@@ -1149,8 +1188,13 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
     const int64_t groups = (tiles + ntile - 1) / max(ntile, 1);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+    TW4_REQUIRE(per_cu >= 0 && per_cu <= 8, TW4_EINVAL, "mma: per_cu in 0 .. 8 (per_cu = %d)", per_cu);
+    TW4_REQUIRE(per_cu == 0 || (splits == 1 && !nin && mt == 1), TW4_EINVAL,
+                "mma: the persistent form takes M <= 16, no split-K and no fused norm");
+    const int64_t cap = static_cast<int64_t>(per_cu) * g_decode_cus[dev];
+    const int64_t units = per_cu > 0 ? (groups < cap ? groups : cap) : groups * splits;
     // x in LDS past kXLdsLimit (one workgroup per CU) only where the grid fits the CUs at once
-    const bool few = groups * splits <= g_decode_cus[dev];
+    const bool few = units <= g_decode_cus[dev];
     if (splits > 1) {
         TW4_REQUIRE(ws && locks, TW4_EINVAL, "mma: split-K needs a workspace and counters");
         TW4_REQUIRE(groups * splits * ntile * mt * 256 <= ws_floats && groups <= n_locks, TW4_ESPACE,
@@ -1166,8 +1210,16 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
         const size_t lds = 16 * (static_cast<size_t>(                                                          \
                                      decode_lds(xlds, M, 128 * R, 0, red_u4, nin != nullptr).total) +          \
                                  1); /* + the split-K flag */                                                  \
-        const unsigned grid = static_cast<unsigned>(groups * splits);                                         \
-        if (splits > 1 && xlds && wide)                                                                        \
+        const unsigned grid = static_cast<unsigned>(units);                                                   \
+        TW4_REQUIRE(per_cu == 0 || xlds, TW4_ECONFIG, "mma: the persistent form stages x in LDS (M = %d, K = %d)", \
+                    M, K);                                                                                     \
+        if (per_cu > 0 && wide)                                                                                \
+            mma_kernel<WK, U, T, 1, kXLdsWide, false, false, true><<<grid, WK * 64, lds, st>>>(                \
+                xp, wp, sp, zp, yp, M, N, K, act, none, ws, locks, splits);                                    \
+        else if (per_cu > 0)                                                                                   \
+            mma_kernel<WK, U, T, 1, kXLds, false, false, true><<<grid, WK * 64, lds, st>>>(                    \
+                xp, wp, sp, zp, yp, M, N, K, act, none, ws, locks, splits);                                    \
+        else if (splits > 1 && xlds && wide)                                                                   \
             mma_kernel<WK, U, T, 1, kXLdsWide, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, \
                                                                                       act, none, ws, locks, splits); \
         else if (splits > 1 && xlds)                                                                           \
@@ -1218,6 +1270,23 @@ extern "C" int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t*
                       reinterpret_cast<const h1*>(scales), reinterpret_cast<const h1*>(zeros), reinterpret_cast<h1*>(y),
                       M, N, K, warps_k, unroll, ntile, act, nullptr, nullptr, nullptr, 0, 0, 1,
                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                               uint16_t* y, int M, int N, int K, int warps_k, int unroll, int ntile, int per_cu, int act,
+                               void* stream) {
+    int rc = check_operands("mma", x, packed, scales, zeros, y, M, N, K);
+    if (rc) return rc;
+    TW4_REQUIRE(M >= 1 && M <= 16, TW4_EINVAL, "mma: the persistent form takes 1 <= M <= 16 (M = %d)", M);
+    TW4_REQUIRE(per_cu >= 1 && per_cu <= 8, TW4_EINVAL, "mma: per_cu in 1 .. 8 (per_cu = %d)", per_cu);
+    TW4_REQUIRE(act == 0 || (act == 1 && N % 16 == 0), TW4_EINVAL,
+                "mma: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
+    rc = ensure_prepared();
+    if (rc) return rc;
+    return mma_launch(reinterpret_cast<const h1*>(x), reinterpret_cast<const u4*>(packed),
+                      reinterpret_cast<const h1*>(scales), reinterpret_cast<const h1*>(zeros), reinterpret_cast<h1*>(y),
+                      M, N, K, warps_k, unroll, ntile, act, nullptr, nullptr, nullptr, 0, 0, 1,
+                      static_cast<hipStream_t>(stream), per_cu);
 }
 
 extern "C" int tw4_mma_splitk(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,

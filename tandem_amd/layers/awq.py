@@ -145,6 +145,8 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 #   ("mmak", warps_k, unroll, ntile, splits)   the same with K split over `splits` workgroups per
 #                                      row-tile group (x in LDS over 1 / splits of K; the last arriver
 #                                      adds the partials, w4_gemm's workspace), M <= 16
+#   ("mmap", warps_k, unroll, ntile, per_cu)   the same with at most per_cu workgroups per CU, each
+#                                      staging x once and streaming several row-tile groups, M <= 16
 #   ("gemm", MT, NT, WARPS_N, WARPS_K, STAGES, SPLITS)   the fused GEMM (below), where it wins
 # warps_k: wavefronts splitting K in a workgroup; unroll: quant groups in flight per lane and
 # iteration; ntile: 16-row tiles per wavefront. Shapes without an entry use DEFAULT_KERNEL.
@@ -350,6 +352,8 @@ class W4Linear(nn.Module):
                     buf, locks = w4_hip.workspace(x.device)
                     return ext.w4_mma_splitk(x, self.packed, self.scales, self.zeros, buf, locks, *cfg,
                                              int(self.silu_mul))
+                if kind == "mmap":  # the matrix-core decode kernel, persistent workgroups
+                    return ext.w4_mma_persist(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
                 if kind != "mma":  # gemv / gemvm past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))

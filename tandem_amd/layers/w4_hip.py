@@ -47,6 +47,7 @@ _SIGNATURES = {
     "tw4_gemv_mfma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma_splitk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tw4_mma_persist": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
@@ -213,6 +214,21 @@ class W4Extension:
         with torch.cuda.device(x.device):
             check(self.lib.tw4_mma(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
                                    int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
+        return y
+
+    def w4_mma_persist(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, per_cu: int,
+                       act: int) -> torch.Tensor:
+        """w4_mma's persistent form (M <= 16, x in LDS): at most per_cu workgroups per CU, each staging
+        x once and streaming several row-tile groups."""
+        m, n, k = check_operands("w4_mma", x, w, s, z)
+        if not 1 <= m <= 16:
+            raise RuntimeError("w4_mma_persist: M <= 16 (one 16-token batch tile)")
+        if act not in (0, 1) or (act and n % 16):
+            raise RuntimeError("w4_mma: act 0, or 1 (SwiGLU) with N % 16 == 0")
+        y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
+        with torch.cuda.device(x.device):
+            check(self.lib.tw4_mma_persist(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k, int(warps_k),
+                                           int(unroll), int(ntile), int(per_cu), int(act), _stream(x)))
         return y
 
     def w4_mma_splitk(self, x, w, s, z, ws, locks, warps_k: int, unroll: int, ntile: int, splits: int,

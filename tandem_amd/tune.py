@@ -95,8 +95,9 @@ def main(argv=None) -> int:
     ap.add_argument("--model", default="qwen3-8b", choices=sorted(MODELS))
     ap.add_argument("--projs", default="", help="comma list of projections (default: all)")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, gemvn, mma, mmak, gemm, dense")
+    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, gemvn, mma, mmak, mmap, gemm, dense")
     ap.add_argument("--splits", default="0,1,2,4,8")
+    ap.add_argument("--per-cu", default="1,2,3,4", help="workgroups per CU of the persistent mma (kind mmap)")
     ap.add_argument("--act", action="store_true", help="time the SwiGLU epilogue (gate_up only)")
     ap.add_argument("--footprint-mb", type=float, default=1024.0)
     ap.add_argument("--out", default="")
@@ -174,6 +175,15 @@ def main(argv=None) -> int:
                     except RuntimeError:  # unroll * batch tiles above 4
                         continue
                     res[("mma", *cfg)] = us
+            if "mmap" in kinds and m <= 16:
+                for cfg in w4_hip.decode_configs():
+                    for pc in (int(v) for v in a.per_cu.split(",")):
+                        try:
+                            us = time_us([lambda w=w, c=cfg, q=pc: ext.w4_mma_persist(x, *w, *c, q, act)
+                                          for w in ws], stream)
+                        except RuntimeError:
+                            continue
+                        res[("mmap", *cfg, pc)] = us
             if "mmak" in kinds and m <= 16:
                 for cfg in w4_hip.decode_configs():
                     for sp in (int(v) for v in a.splits.split(",")):

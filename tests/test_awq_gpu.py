@@ -295,6 +295,32 @@ def test_mma_split_k_every_config(ext):
     assert ran > 3 * len(DECODE_CONFIGS)
 
 
+def test_mma_persistent_matches_mma(ext):
+    """The persistent form of the matrix-core decode kernel (tw4_mma_persist): workgroups that
+    stream 1 to 5 row-tile groups each (N past 256 CUs x 16 rows x ntile, partial last tile),
+    every compiled config, 1 to 4 workgroups per CU, plain and SwiGLU: bit for bit the one-pass
+    kernel's output (same chunk order and reduction), and within tolerance of the oracle."""
+    ran = 0
+    for k, n, interleave in ((1024, 16392, False), (4096, 8200, False), (1024, 16384, True)):
+        c = Case(k, n, seed=25, interleave=interleave)
+        for m in (1, 8, 16):
+            x = c.x(m, seed=900 + m)
+            xg = gpu(x)
+            ref = o.swiglu_reference(x, c.w_exact) if interleave else o.linear(x, c.w_exact)
+            for cfg in DECODE_CONFIGS:
+                one = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, int(interleave))
+                for per_cu in (1, 2, 4):
+                    if per_cu > 1 and m * (2 * k + 16) > 80 * 1024:  # x fits in LDS only at one per CU
+                        with pytest.raises(RuntimeError, match="persistent form stages x in LDS"):
+                            ext.w4_mma_persist(xg, c.packed, c.s, c.zz, *cfg, per_cu, int(interleave))
+                        continue
+                    y = ext.w4_mma_persist(xg, c.packed, c.s, c.zz, *cfg, per_cu, int(interleave))
+                    ran += 1
+                    assert torch.equal(y, one), (k, n, m, cfg, per_cu, interleave)
+            check_close(one, ref, 0.02, 0.01, (k, n, m, interleave))
+    assert ran == (3 * 3 * 3 - 2) * len(DECODE_CONFIGS)
+
+
 def test_mma_split_k_deterministic_and_graph_replay(ext):
     """Split-K decode: identical bits on every call (the partials are added in split order), and
     correct on every replay of a captured graph with eager work in between."""

@@ -91,6 +91,12 @@ def test_argument_errors_return_before_launch():
                                     17, 64, 1024, 4, 2, 1, 2, 0, None), "M <= 16"),
         (lambda: lib.tw4_mma_splitk(_fake(), _fake(), _fake(), _fake(), _fake(), None, _fake(), 1 << 20, 1024,
                                     8, 64, 1024, 4, 2, 1, 2, 0, None), "workspace"),
+        (lambda: lib.tw4_mma_persist(_fake(), _fake(), _fake(), _fake(), _fake(), 17, 64, 1024, 4, 2, 1, 1, 0, None),
+         "M <= 16"),
+        (lambda: lib.tw4_mma_persist(_fake(), _fake(), _fake(), _fake(), _fake(), 8, 64, 1024, 4, 2, 1, 0, 0, None),
+         "per_cu"),
+        (lambda: lib.tw4_mma_persist(_fake(), _fake(), _fake(), _fake(), _fake(), 8, 24, 1024, 4, 2, 1, 1, 1, None),
+         "SwiGLU"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
                               32, 64, 128, 2, 1, 4, 1, 2, 17, 0, None), "splits"),
         (lambda: lib.tw4_gemm(_fake(), _fake(), _fake(), _fake(), _fake(), _fake(), _fake(), 1 << 20, 1024,
@@ -225,6 +231,9 @@ def test_tables_are_well_formed():
                 assert len(cfg) == 7 and tuple(cfg[1:6]) in gemm and 0 <= cfg[6] <= 16
             elif cfg[0] == "mmak":  # a compiled decode config and 2 .. 16 K splits (at most one per group)
                 assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 2 <= cfg[4] <= min(16, k // 128)
+            elif cfg[0] == "mmap":  # a compiled decode config, 1 .. 8 workgroups per CU, x in LDS
+                assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 1 <= cfg[4] <= 8
+                assert m * (2 * k + 16) <= 136 * 1024  # past 80 KB only for grids of at most one per CU
             else:  # a compiled decode config; gemv / gemvm only where they run (M <= 4)
                 assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
                 assert cfg[0] == "mma" or m <= 4
