@@ -297,12 +297,13 @@ def test_mma_split_k_every_config(ext):
 
 def test_mma_persistent_matches_mma(ext):
     """The persistent form of the matrix-core decode kernel (tw4_mma_persist): workgroups that
-    stream 1 to 5 row-tile groups each (N past 256 CUs x 16 rows x ntile, partial last tile),
+    stream 1 to 5 row-tile groups each (N past 256 CUs x 16 rows x ntile, partial last tile, K
+    not a multiple of warps_k quant groups),
     every compiled config, 1 to 4 workgroups per CU, plain and SwiGLU: bit for bit the one-pass
     kernel's output (same chunk order and reduction), and within tolerance of the oracle."""
     ran = 0
-    for k, n, interleave in ((1024, 16392, False), (4096, 8200, False), (1024, 16384, True)):
-        c = Case(k, n, seed=25, interleave=interleave)
+    for k, n, interleave in ((1024, 16392, False), (4096, 8200, False), (2560, 8208, False), (1024, 16384, True)):
+        c = Case(k, n, seed=25, interleave=interleave)  # K = 2560: 20 groups, uneven wavefront ranges
         for m in (1, 8, 16):
             x = c.x(m, seed=900 + m)
             xg = gpu(x)
@@ -318,7 +319,7 @@ def test_mma_persistent_matches_mma(ext):
                     ran += 1
                     assert torch.equal(y, one), (k, n, m, cfg, per_cu, interleave)
             check_close(one, ref, 0.02, 0.01, (k, n, m, interleave))
-    assert ran == (3 * 3 * 3 - 2) * len(DECODE_CONFIGS)
+    assert ran == (4 * 3 * 3 - 4) * len(DECODE_CONFIGS)
 
 
 def test_mma_split_k_deterministic_and_graph_replay(ext):
