@@ -874,8 +874,8 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int tg_next = tg + static_cast<int>(gridDim.x);
     const bool more = PERSIST && tg_next < ngroups;  // uniform across the workgroup
     // The streams the pass's last chunk prefetches from. Last pass: weight blocks of an empty buffer
-    // range (out-of-range buffer loads return zeros without a memory access) and the current tile
-    // group's group parameters, already cached.
+    // range (out-of-range buffer loads return zeros without a memory access) and the group
+    // parameters the chunk itself has just loaded (cache hits).
     TileStreams<NT> tsn = ts;
     if constexpr (PERSIST) {
         if (more) {
@@ -903,11 +903,11 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     if (i + 2 == nch) {
         mma_chunk<true, XM, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge,
                                        glo, kb, magic);
-        mma_chunk<PERSIST, XM, U, NT, MT, false>(b, a, tsn, gb, s16, z16, smem, l, xl, xrow, acc, gb + U * (i + 1), ge,
-                                                 glo, kb, magic);
+        mma_chunk<PERSIST, XM, U, NT, MT, false>(b, a, tsn, more ? gb : gb + U * (i + 1), s16, z16, smem, l, xl, xrow,
+                                                 acc, gb + U * (i + 1), ge, glo, kb, magic);
     } else if (i + 1 == nch) {
-        mma_chunk<PERSIST, XM, U, NT, MT, false>(a, b, tsn, gb, s16, z16, smem, l, xl, xrow, acc, gb + U * i, ge, glo,
-                                                 kb, magic);
+        mma_chunk<PERSIST, XM, U, NT, MT, false>(a, b, tsn, more ? gb : gb + U * i, s16, z16, smem, l, xl, xrow, acc,
+                                                 gb + U * i, ge, glo, kb, magic);
         if constexpr (PERSIST) a = b;
     }
     if constexpr (NORM) write_residual<false>(xg, nin, kx, xsl, lane);
