@@ -11,6 +11,18 @@ then reads, per dispatch, the HBM bytes the kernel moved:
     rocprofv3 --pmc FETCH_SIZE -d <dir> -o run --output-format csv -- python3 -m tandem_amd.prof
     rocprofv3 --pmc WRITE_SIZE -d <dir> -o run --output-format csv -- python3 -m tandem_amd.prof
     python -m tandem_amd.prof --summarize <fetch counter_collection.csv> <write counter_collection.csv>
+
+The same launches give the GEMM's matrix-core utilisation (M > 16; --cfg forces one GEMM
+configuration, mt,nt,warps_n,warps_k,stages,splits, in place of the table's, to compare tile and
+split-K choices on the same shape):
+
+    rocprofv3 --kernel-trace --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_F16 -d <dir> -o run \
+        --output-format csv -- python3 -m tandem_amd.prof --proj gate_up --m 32 [--cfg 2,1,4,2,2,1]
+    python -m tandem_amd.prof --proj gate_up --m 32 --summarize-mfma <counter_collection.csv>
+
+MfmaUtil is rocprofiler's derived counter: the SIMDs' summed SQ_VALU_MFMA_BUSY_CYCLES over
+GRBM_GUI_ACTIVE x the number of SIMDs, in percent. SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 is the fp16
+matrix-core work issued, which against 2 M N K shows the padding of the token tiles.
 """
 
 from __future__ import annotations
@@ -52,6 +64,8 @@ def run(a: argparse.Namespace) -> int:
         lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32, generator=g))
         lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
         lin.finalize(torch.cuda.get_device_name(dev))
+        if a.cfg:
+            lin.gemm_kernels[(n, k)] = ((1 << 30, tuple(int(v) for v in a.cfg.split(","))),)
         layers.append(lin)
     x = torch.randn(a.m, k, device=dev, dtype=torch.float16)
     torch.cuda.synchronize()
@@ -59,7 +73,7 @@ def run(a: argparse.Namespace) -> int:
         layers[i % copies](x)
     torch.cuda.synchronize()
     print(f"prof: {a.copies} copies of {a.copy_mib} MiB, {a.launches} x {a.proj} (K {k}, N {n}) M={a.m} "
-          f"over {copies} weight copies", flush=True)
+          f"over {copies} weight copies, gemm config {a.cfg or 'from the table'}", flush=True)
     return 0
 
 
@@ -114,6 +128,35 @@ def summarize(fetch_csv: str, write_csv: str, copy_mib: int, copies: int, algori
     return rec
 
 
+def summarize_mfma(path: str, m: int, n: int, k: int) -> dict:
+    """Per tw4 kernel: average MfmaUtil (%) and fp16 MFMA work per dispatch (SQ_INSTS_VALU_MFMA_MOPS_F16
+    x 512 flops) against the algorithmic 2 M N K, plus the dispatch's duration where the file has
+    timestamps (a --kernel-trace run of the same command)."""
+    util, mops = _per_kernel(path, "MfmaUtil"), _per_kernel(path, "SQ_INSTS_VALU_MFMA_MOPS_F16")
+    dur: dict[str, list[float]] = {}
+    with open(path, newline="", encoding="utf-8") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") == "MfmaUtil" and row.get("Start_Timestamp") and row.get("End_Timestamp"):
+                dur.setdefault(row["Kernel_Name"], []).append(
+                    (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    alg = 2 * m * n * k
+    rows = {}
+    for name, v in util.items():
+        if "tw4" not in name:
+            continue
+        mv = [val for _, val in mops.get(name, [])]
+        flops = 512 * sum(mv) / len(mv) if mv else None
+        row = {"dispatches": len(v), "MfmaUtil_pct": round(sum(val for _, val in v) / len(v), 2),
+               "mfma_flops": flops, "algorithmic_flops": alg,
+               "mfma_over_algorithmic": round(flops / alg, 4) if flops else None}
+        if dur.get(name):
+            us = sum(dur[name]) / len(dur[name])
+            row["us_under_counters"] = round(us, 2)
+            row["algorithmic_tflops_under_counters"] = round(alg / us / 1e6, 1)
+        rows[name] = row
+    return {"m": m, "n": n, "k": k, "kernels": rows}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--proj", default="gate_up", choices=sorted(SHAPES))
@@ -121,8 +164,14 @@ def main(argv=None) -> int:
     ap.add_argument("--launches", type=int, default=40)
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--cfg", default="", help="GEMM config mt,nt,warps_n,warps_k,stages,splits for every M > 16")
     ap.add_argument("--summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--summarize-mfma", metavar="COUNTER_CSV")
     a = ap.parse_args(argv)
+    if a.summarize_mfma:
+        k, n = SHAPES[a.proj]
+        print(json.dumps(summarize_mfma(a.summarize_mfma, a.m, n, k), indent=1))
+        return 0
     if a.summarize:
         k, n = SHAPES[a.proj]
         g = k // 128
