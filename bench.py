@@ -1,6 +1,7 @@
 """Benchmark of the MI355X AWQ W4A16 linear path on Qwen3-8B shapes (one GPU).
 
     python bench.py [--steps K] [--warmup W] [--m 1] [--layers 36] [--no-cpu] [--no-detail]
+    python bench.py --sweep [--sweep-out FILE]
 
 One step = one decode token's W4A16 linears of the whole Qwen3-8B stack: 36 layers x {qkv
 (K 4096, N 6144), o (4096, 4096), gate_up (4096, 24576), down (12288, 4096)} at M = 1, launched
@@ -24,6 +25,13 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
   decode_step   the model's decode step (tandem_amd.model: norms, one-token attention, SwiGLU
                 gate_up, lm_head) replayed from the bucketed HIP graphs of tandem_amd.decode_graph,
                 M in {1, 8, 32}: us per step, tokens/s, GB/s of the step's weight bytes
+
+--sweep times every single-linear configuration of the benchmark's configs instead (Qwen3-0.6B
+qkv at M = 1; Qwen3-8B's four shapes at M in {1, 4, 8, 16} and {24, 32, 64, 256, 1024, 4096};
+Qwen3-1.7B's four shapes at M in {1, 4, 8}): one JSON line per (shape, M) with us/call, GB/s,
+TFLOP/s, % of the roofline max(B / 8 TB/s, 2 M N K / 2.5 PFLOP/s), the kernel that ran, and past
+M = 16 the dequantize + torch.matmul comparator. Each shape rotates over enough weight copies
+(>= 1 GB) that every call streams from HBM.
 """
 
 from __future__ import annotations
@@ -40,6 +48,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, AMD public spec
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, AMD public spec
 QWEN3_8B = (("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576), ("down", 12288, 4096))
+QWEN3_1_7B = (("qkv", 2048, 4096), ("o", 2048, 2048), ("gate_up", 2048, 12288), ("down", 6144, 2048))
+SWEEP = ((("Qwen3-0.6B", "qkv", 1024, 4096), (1,)),) + tuple(
+    (("Qwen3-8B", p, k, n), (1, 4, 8, 16, 24, 32, 64, 256, 1024, 4096)) for p, k, n in QWEN3_8B) + tuple(
+    (("Qwen3-1.7B", p, k, n), (1, 4, 8)) for p, k, n in QWEN3_1_7B)
 LM_HEAD = (4096, 151936)  # Qwen3-8B vocabulary x hidden, fp16
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_m1.json")
 
@@ -59,6 +71,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-detail", action="store_true", help="skip the per-projection sweep")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--sweep", action="store_true", help="time every (shape, M) of the configs; JSON line each")
+    ap.add_argument("--sweep-out", default="", help="also append the sweep's JSON lines to this file")
     ap.add_argument("--step-only", action="store_true",
                     help="only the decode_step section (for profiling the whole step); prints its JSON")
     return ap.parse_args()
@@ -123,6 +137,53 @@ def kernel_of(awq, lin, m: int) -> str:
     if cfg is None or not awq.FUSED_GEMM:
         return "dequant+matmul"
     return f"mma{tuple(cfg[1:])}" if cfg[0] == "mma" else f"gemm{cfg}"
+
+
+def random_linear(torch, awq, k: int, n: int, dev, g):
+    """One W4Linear with random AutoAWQ weights (uniform int4 q and z, fp16 scales in [0.001, 0.02]),
+    repacked by the product's finalize."""
+    lin = awq.W4Linear(k, n, 128).to(dev)
+    lin.qweight.copy_(torch.randint(-2**31, 2**31 - 1, lin.qweight.shape, device=dev, dtype=torch.int32, generator=g))
+    lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32, generator=g))
+    lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
+    lin.finalize(torch.cuda.get_device_name(dev))
+    return lin
+
+
+def sweep(torch, awq, dev, stream, out_path: str) -> int:
+    """Per (shape, M): us/call over C weight copies (>= 1 GB in all) replayed from one HIP graph."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    for (model, proj, k, n), ms in SWEEP:
+        copies = min(512, max(2, -(-(1 << 30) // (n * k // 2))))
+        lins = [random_linear(torch, awq, k, n, dev, g) for _ in range(copies)]
+        for m in ms:
+            x = torch.randn(m, k, device=dev, dtype=torch.float16)
+            gr = graph_of(torch, lambda: [lin(x) for lin in lins], stream)
+            est = time_graph(torch, gr, stream, reps=1)  # one replay, to size the timed run to ~20 ms
+            us = time_graph(torch, gr, stream, reps=max(2, min(50, int(0.02 / est)))) / copies * 1e6
+            del gr
+            b, f = call_bytes(m, k, n), 2 * m * k * n
+            roof_us = max(b / HBM_PEAK_GBS / 1e3, f / FP16_PEAK_TFLOPS / 1e6)
+            rec = {"model": model, "proj": proj, "K": k, "N": n, "M": m, "us": round(us, 2),
+                   "GBps": round(b / us / 1e3, 1), "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1),
+                   "TFLOPs": round(f / us / 1e6, 2), "bound": "hbm" if b / HBM_PEAK_GBS / 1e3 >= roof_us else "mfma",
+                   "pct_roofline": round(roof_us / us * 100, 1), "kernel": kernel_of(awq, lins[0], m)}
+            if m > 16:  # the dequantize-then-fp16-GEMM comparator (HIP dequant + torch.matmul)
+                sub = lins[:min(copies, 16)]
+                dg = graph_of(torch, lambda: [lin._dense(x) for lin in sub], stream)
+                rec["dequant_matmul_us"] = round(time_graph(torch, dg, stream, reps=2) / len(sub) * 1e6, 2)
+                rec["speedup_vs_dequant_matmul"] = round(rec["dequant_matmul_us"] / us, 2)
+                del dg
+            line = json.dumps(rec)
+            print(line, flush=True)
+            if out_path:
+                with open(out_path, "a", encoding="utf-8") as fo:
+                    fo.write(line + "\n")
+            del x
+        del lins
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return 0
 
 
 def cpu_baseline(budget_s: float, m: int) -> dict:
@@ -223,6 +284,8 @@ def main() -> int:
     if a.step_only:
         print(json.dumps({"decode_step": decode_step(torch, dev)}), flush=True)
         return 0
+    if a.sweep:
+        return sweep(torch, awq, dev, torch.cuda.Stream(dev), a.sweep_out)
     m = a.m
     layers = make_layers(torch, awq, a.layers, dev)
     stream = torch.cuda.Stream(dev)

@@ -555,3 +555,16 @@ def test_w4linear_qwen3_8b_tables(proj, silu):
             check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, (proj, m))
         else:
             check_close(y, o.linear(x, c.w_exact), 0.05, 0.02, (proj, m))
+
+
+def test_w4linear_qwen3_0_6b_qkv_table():
+    """The Qwen3-0.6B fused qkv shape (K 1024, N 4096, the reference's CPU-runnable config) through
+    the gfx950 decode table's own entries (gemv at M = 1, gemvm at 2 .. 4, mma at 5 .. 8) and the
+    default kernels past them, against the oracle's dequantize-then-matmul."""
+    layer, c = _layer(1024, 4096, seed=61)
+    rng = np.random.default_rng(29)
+    for m in (1, 2, 4, 5, 8, 9, 16, 32):
+        if m <= 8:
+            assert (4096, 1024, m) in layer.kernels, m
+        x = rng.standard_normal((m, 1024)).astype(np.float16)
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, ("0.6b qkv", m))
