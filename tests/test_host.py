@@ -328,3 +328,24 @@ def test_staging_indices_in_bounds(k):
                         if n and f < n:  # the exact position of a real chunk
                             assert (mm, c) == divmod(f, n16)
                             assert mm * g_count + (c0 + c) // 16 < m * g_count
+
+
+def test_bench_sweep_covers_the_single_linear_configs():
+    """bench.py --sweep times every single-linear (shape, M) of the benchmark configs: Qwen3-0.6B qkv
+    at M = 1, Qwen3-8B's four shapes at the decode and GEMM M lists, Qwen3-1.7B's at M = 1, 4, 8."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    got = {(model, proj, k, n, m) for (model, proj, k, n), ms in bench.SWEEP for m in ms}
+    want = {("Qwen3-0.6B", "qkv", 1024, 4096, 1)}
+    want |= {("Qwen3-8B", p, k, n, m) for p, (k, n) in {"qkv": (4096, 6144), "o": (4096, 4096),
+                                                        "gate_up": (4096, 24576), "down": (12288, 4096)}.items()
+             for m in (1, 4, 8, 16, 24, 32, 64, 256, 1024, 4096)}
+    want |= {("Qwen3-1.7B", p, k, n, m) for p, (k, n) in {"qkv": (2048, 4096), "o": (2048, 2048),
+                                                          "gate_up": (2048, 12288), "down": (6144, 2048)}.items()
+             for m in (1, 4, 8)}
+    assert got == want
+    # the per-call byte count of the benchmark's metric: int4 weights, fp16 scales, int4 zeros, x and y
+    assert bench.call_bytes(1, 4096, 24576) == 52355072
