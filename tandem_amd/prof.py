@@ -64,8 +64,8 @@ def run(a: argparse.Namespace) -> int:
         lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32, generator=g))
         lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
         lin.finalize(torch.cuda.get_device_name(dev))
-        if a.cfg:
-            lin.gemm_kernels[(n, k)] = ((1 << 30, tuple(int(v) for v in a.cfg.split(","))),)
+        if a.cfg:  # a per-layer copy: the module-level table is shared by every W4Linear
+            lin.gemm_kernels = {**lin.gemm_kernels, (n, k): ((1 << 30, tuple(int(v) for v in a.cfg.split(","))),)}
         layers.append(lin)
     x = torch.randn(a.m, k, device=dev, dtype=torch.float16)
     torch.cuda.synchronize()
