@@ -91,6 +91,24 @@ def dequant_exact(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, g
     return np.ascontiguousarray(w.T)
 
 
+def dequant_exact_rows(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, rows,
+                       group: int = GROUP) -> np.ndarray:
+    """dequant_exact(...)[rows] without unpacking the whole matrix: output feature n is nibble
+    AWQ_REVERSE_ORDER[n % 8] of word column n // 8 (python/tandem/layers/awq.py:38-46), for the
+    sampled-column checks at full size (a [24576, 4096] weight unpacked whole is 400 MB)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    shifts = 4 * np.asarray(AWQ_REVERSE_ORDER, dtype=np.int64)[rows % 8]
+    qw = np.asarray(qweight).astype(np.int64)[:, rows // 8] & 0xFFFFFFFF     # [K, R]
+    qz = np.asarray(qzeros).astype(np.int64)[:, rows // 8] & 0xFFFFFFFF      # [K/G, R]
+    q = ((qw >> shifts) & 0xF).astype(np.float32)
+    z = ((qz >> shifts) & 0xF).astype(np.float32)
+    s = np.asarray(scales)[:, rows].astype(np.float32)
+    if q.shape[0] % group or z.shape[0] * group != q.shape[0] or s.shape != z.shape:
+        raise ValueError(f"dequant: qweight {q.shape} qzeros {z.shape} scales {s.shape} group {group}")
+    w = (q - np.repeat(z, group, axis=0)) * np.repeat(s, group, axis=0)
+    return np.ascontiguousarray(w.T)
+
+
 def dequant(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray, group: int = GROUP) -> np.ndarray:
     """Dense fp16 [N, K] (nn.Linear layout) = fp16_rne((q - z) * s): float32 math, then one cast to
     fp16 with round-to-nearest-even (python/tandem/layers/awq.py:110-119, `w.to(out dtype)`)."""

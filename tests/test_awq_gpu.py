@@ -540,15 +540,17 @@ def test_w4linear_gemm_switch_off(monkeypatch):
     check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, "switch off")
 
 
-@pytest.mark.parametrize("proj,silu", [("gate_up", True), ("gate_up", False), ("down", False), ("qkv", False)])
+@pytest.mark.parametrize("proj,silu", [("gate_up", True), ("gate_up", False), ("down", False), ("qkv", False),
+                                       ("o", False)])
 def test_w4linear_qwen3_8b_tables(proj, silu):
     """W4Linear at the real Qwen3-8B shapes through the gfx950 tables, across the M ranges where
-    the tables switch kernels (gemv, mma, the GEMM with and without split-K)."""
+    the tables switch kernels (gemv, gemvm, mma and its split-K and persistent forms, the GEMM with
+    and without split-K): every M of the benchmark's decode sweep and its M = 24 / 32 / 64 entries."""
     k, n = QWEN3_8B[proj]
     layer, c = _layer(k, n, seed=SEEDS[proj] + 10, silu_mul=silu)
     assert layer.kernels is awq.W4_KERNELS[awq.GFX950] and layer.gemm_kernels is awq.W4_GEMM_KERNELS[awq.GFX950]
     rng = np.random.default_rng(23)
-    for m in (1, 2, 5, 8, 16, 24, 48, 130):
+    for m in (1, 2, 4, 5, 7, 8, 12, 16, 24, 32, 48, 64, 130):
         x = rng.standard_normal((m, k)).astype(np.float16)
         y = layer(gpu(x))
         if silu:

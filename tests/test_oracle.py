@@ -124,6 +124,29 @@ def test_dequant_rejects_bad_group():
         o.dequant(qw[:200], qz, s)
 
 
+def test_dequant_exact_rows_sampled_columns():
+    """dequant_exact_rows (the full-size tests' sampled output features) against the committed
+    fixture's fp16 weights, the rational product at single entries, and a copy that takes the pack
+    order for the reverse order (a plausible slip), which the fixture must reject."""
+    data = np.load(os.path.join(GOLDEN, "awq_small.npz"))
+    n = data["w_fp16"].shape[0]
+    rows = np.array([0, 1, 7, 8, n - 1, 3, 3], dtype=np.int64)  # repeats and any order
+    got = o.dequant_exact_rows(data["qweight"], data["qzeros"], data["scales"], rows)
+    assert (got.astype(np.float16).view(np.uint16) == data["w_fp16"][rows].view(np.uint16)).all()
+    qw, qz, s, q, z = o.random_awq(384, 40, seed=12)
+    sel = np.array([39, 0, 17, 22])
+    w = o.dequant_exact_rows(qw, qz, s, sel)
+    for i, n_ in enumerate(sel):
+        for k in (0, 127, 128, 383):
+            exact = Fraction(int(q[k, n_]) - int(z[k // 128, n_])) * Fraction(float(s[k // 128, n_]))
+            assert Fraction(float(w[i, k])) == exact
+    shifts = 4 * np.asarray(o.AWQ_PACK_ORDER)[rows % 8]  # the slip: nibble PACK[j] instead of REVERSE[j]
+    qq = (data["qweight"].astype(np.int64)[:, rows // 8] & 0xFFFFFFFF) >> shifts & 0xF
+    zz = (data["qzeros"].astype(np.int64)[:, rows // 8] & 0xFFFFFFFF) >> shifts & 0xF
+    bad = ((qq - np.repeat(zz, 128, 0)) * np.repeat(data["scales"][:, rows].astype(np.float32), 128, 0)).T
+    assert not (bad.astype(np.float16).view(np.uint16) == data["w_fp16"][rows].view(np.uint16)).all()
+
+
 # ---------------------------------------------------------------- interleave (awq.py:71-75)
 def test_interleave_closed_form():
     """Row 16 T + 8 h + i of the interleaved tensor is source row h N/2 + 8 T + i."""
