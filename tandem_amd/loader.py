@@ -1,22 +1,30 @@
-"""AutoAWQ checkpoint loading and the model wiring of the W4A16 linears.
+"""Put an AutoAWQ "gemm" checkpoint into a model built from W4Linear (and nn.Linear) projections.
 
-The counterpart of the parts of 12vivi/tandem that put a real AutoAWQ checkpoint through the op:
+Behaviour kept from 12vivi/tandem (python/tandem/model_config.py:28-43 for ``QuantConfig``,
+python/tandem/models/loader.py:66-105 for ``load_weights``):
 
-    QuantConfig              quantization_config of config.json      python/tandem/model_config.py:28-43
-    load_weights             safetensors -> parameters and AWQ        python/tandem/models/loader.py:14-105
-                             buffers, fused q/k/v and gate/up
+- only 4-bit AWQ "gemm" checkpoints with zero points are accepted; anything else raises
+  NotImplementedError, and an absent quantization_config means an unquantized model;
+- the model's fused projections take their halves from the checkpoint's separate ones
+  (q / k / v -> qkv_proj, gate / up -> gate_up_proj), in that order along the output features;
+- a tensor the model has no use for is logged and skipped (a stored lm_head of a tied-embedding
+  model silently); a model tensor the checkpoint cannot fill raises RuntimeError; a shape that does
+  not fit raises ValueError; a directory without *.safetensors raises FileNotFoundError.
 
-A checkpoint stores q_proj / k_proj / v_proj and gate_proj / up_proj separately; the model holds
-one fused qkv_proj and gate_up_proj. Dense weights are fused along their rows; the AutoAWQ
-tensors (qweight [K, N/8], qzeros [K/G, N/8], scales [K/G, N]) carry the output dimension second,
-so they are fused along their columns: shard offsets are taken from the fused size (q first, k and
-v sharing the remainder; gate and up halves). Loading is host work on CPU tensors; the W4Linear
-layers are then moved to the GPU and repacked by ``finalize_quantized`` (``tandem_amd.model.prepare``).
-The model classes, with the SwiGLU wiring of the MLP, are in ``tandem_amd.model``.
+How this module does it: the model drives the load. ``load_weights`` first indexes the tensor names
+of every shard file (reading no data), then asks, for each tensor the model owns, where its data
+comes from (``plan_sources``): a checkpoint tensor of the same name, or the list of per-projection
+tensors that stacked along the output dimension make it up. The output dimension is dim 0 of a
+dense weight or bias and dim 1 of the AutoAWQ tensors (qweight [K, N/8], qzeros [K/G, N/8],
+scales [K/G, N]), so ``fused_sources`` records the axis with the names. Every plan is checked
+(sources present, stacked shape equal to the target's) before any data is copied. Loading is host
+work on CPU tensors; the layers are moved to the GPU and repacked afterwards by
+``finalize_quantized`` (see ``tandem_amd.model.prepare``).
 """
 
 from __future__ import annotations
 
+import contextlib
 import glob
 import logging
 import os
@@ -27,106 +35,122 @@ from typing import Any, Optional
 import torch
 from torch import nn
 
-
 logger = logging.getLogger(__name__)
 
+AWQ_TENSORS = ("qweight", "qzeros", "scales")
 
-@dataclass
+
+@dataclass(frozen=True)
 class QuantConfig:
-    """Weight-only quantization of a checkpoint (``quantization_config`` in config.json)."""
+    """The ``quantization_config`` entry of a checkpoint's config.json, for weight-only AWQ."""
 
-    method: str  # "awq"
+    method: str
     bits: int
     group_size: int
 
     @classmethod
     def from_dict(cls, d: Optional[dict[str, Any]]) -> Optional["QuantConfig"]:
-        """None for an unquantized model; 4-bit AutoAWQ "gemm" with zero points, else
-        NotImplementedError (python/tandem/model_config.py:35-43)."""
+        """None when the checkpoint is not quantized. Accepts AutoAWQ's 4-bit "gemm" packing with
+        zero points (``version`` and ``zero_point`` may be absent: those are AutoAWQ's defaults) and
+        raises NotImplementedError, naming what does not fit, for every other scheme."""
         if not d:
             return None
-        if (d.get("quant_method") == "awq" and d.get("bits") == 4 and d.get("zero_point", True)
-                and str(d.get("version", "gemm")).lower() == "gemm"):
-            return cls("awq", 4, int(d.get("group_size", 128)))
-        raise NotImplementedError(f"unsupported quantization_config: {d} (4-bit AWQ 'gemm' checkpoints only)")
+        reasons = []
+        if d.get("quant_method") != "awq":
+            reasons.append(f"quant_method {d.get('quant_method')!r} (only 'awq')")
+        if d.get("bits") != 4:
+            reasons.append(f"bits {d.get('bits')!r} (only 4)")
+        if not d.get("zero_point", True):
+            reasons.append("symmetric quantization (AutoAWQ zero points expected)")
+        if str(d.get("version", "gemm")).lower() != "gemm":
+            reasons.append(f"packing {d.get('version')!r} (only 'gemm')")
+        if reasons:
+            raise NotImplementedError(f"cannot load quantization_config {d}: " + "; ".join(reasons))
+        return cls("awq", 4, int(d.get("group_size", 128)))
 
 
-_IGNORED = re.compile(r"(rotary_emb\.inv_freq|\.attn\.bias|\.masked_bias)$")
-_AWQ_SUFFIXES = (".qweight", ".qzeros", ".scales")
-# checkpoint tensors that fill a slice of a fused model tensor: (pattern, fused name, shard order)
-_STACKED = (
-    (re.compile(r"^(.*\.self_attn)\.(q|k|v)_proj\.(weight|bias|qweight|qzeros|scales)$"), "qkv_proj", ("q", "k", "v")),
-    (re.compile(r"^(model\.layers\.\d+\.mlp)\.(gate|up)_proj\.(weight|qweight|qzeros|scales)$"), "gate_up_proj",
-     ("gate", "up")),
+# Model tensors assembled from several checkpoint tensors: (model-name pattern, parts in stacking
+# order). The attention prefix may sit anywhere in the module tree; the MLP pattern names the
+# dense decoder MLP only (a mixture-of-experts layer's "mlp.experts.E.*" never matches).
+_FUSED = (
+    (re.compile(r"^(?P<pre>.+\.self_attn)\.qkv_proj\.(?P<t>weight|bias|qweight|qzeros|scales)$"),
+     ("q_proj", "k_proj", "v_proj")),
+    (re.compile(r"^(?P<pre>model\.layers\.\d+\.mlp)\.gate_up_proj\.(?P<t>weight|qweight|qzeros|scales)$"),
+     ("gate_proj", "up_proj")),
 )
+# Checkpoint tensors that are never model state (buffers older exporters saved).
+_NOT_STATE = ("rotary_emb.inv_freq", ".attn.bias", ".masked_bias")
 
 
-def stacked_target(name: str) -> Optional[tuple[str, str, tuple[str, ...]]]:
-    """Checkpoint name -> (fused tensor name, shard, all shards), or None."""
-    for pattern, fused, shards in _STACKED:
-        m = pattern.match(name)
-        if m:
-            return f"{m.group(1)}.{fused}.{m.group(3)}", m.group(2), shards
+def fused_sources(target: str) -> Optional[tuple[list[str], int]]:
+    """(checkpoint names in stacking order, stacking axis) of a fused model tensor, else None."""
+    for pattern, parts in _FUSED:
+        hit = pattern.match(target)
+        if hit:
+            kind = hit.group("t")
+            return [f"{hit.group('pre')}.{p}.{kind}" for p in parts], 1 if kind in AWQ_TENSORS else 0
     return None
 
 
-def copy_shard(dst: torch.Tensor, src: torch.Tensor, shard: str, shards: tuple[str, ...], name: str) -> None:
-    """Copy one shard into its slice of the fused tensor: rows for dense tensors, columns for the
-    AutoAWQ ones (python/tandem/models/loader.py:41-58)."""
-    if name.endswith(_AWQ_SUFFIXES):
-        dst, src = dst.t(), src.t()
-    rows, total = src.shape[0], dst.shape[0]
-    if shards == ("q", "k", "v"):
-        start = {"q": 0, "k": total - 2 * rows, "v": total - rows}[shard]
-    else:
-        start = {"gate": 0, "up": rows}[shard]
-    if start < 0 or start + rows > total or tuple(src.shape[1:]) != tuple(dst.shape[1:]):
-        raise ValueError(f"shape mismatch for {name}: checkpoint {tuple(src.shape)} vs fused {tuple(dst.shape)}")
-    with torch.no_grad():
-        dst[start:start + rows].copy_(src.to(dst.dtype))
+def model_tensors(model: nn.Module) -> dict[str, torch.Tensor]:
+    """What a checkpoint fills: every parameter, and the AutoAWQ buffers W4Linear registers."""
+    out = dict(model.named_parameters())
+    out.update((n, b) for n, b in model.named_buffers() if n.rsplit(".", 1)[-1] in AWQ_TENSORS)
+    return out
+
+
+def plan_sources(targets: dict[str, torch.Tensor], available: set[str]
+                 ) -> tuple[dict[str, tuple[list[str], int]], list[str]]:
+    """For each target: (checkpoint names, stacking axis), the same-named tensor first, else the
+    fused parts. Returns (plans, targets the checkpoint cannot fill)."""
+    plans, missing = {}, []
+    for name in targets:
+        if name in available:
+            plans[name] = ([name], 0)
+            continue
+        fused = fused_sources(name)
+        if fused is not None and all(src in available for src in fused[0]):
+            plans[name] = fused
+        else:
+            missing.append(name)
+    return plans, missing
+
+
+def _stacked_shape(shapes: list[tuple[int, ...]], axis: int) -> Optional[tuple[int, ...]]:
+    first = shapes[0]
+    if any(len(s) != len(first) or s[:axis] + s[axis + 1:] != first[:axis] + first[axis + 1:] for s in shapes):
+        return None
+    return first[:axis] + (sum(s[axis] for s in shapes),) + first[axis + 1:]
 
 
 def load_weights(model: nn.Module, model_path: str) -> None:
-    """Every parameter, and the AWQ buffers of quantized layers (qweight / qzeros / scales, which
-    the W4Linear constructor registers), from the *.safetensors files of ``model_path``. Unknown
-    checkpoint tensors are reported and skipped; a parameter or buffer left unfilled raises."""
+    """Fill every parameter of ``model`` and the AutoAWQ buffers of its W4Linear layers from the
+    *.safetensors files in ``model_path`` (CPU tensors, cast to each target's dtype)."""
     from safetensors import safe_open
 
     files = sorted(glob.glob(os.path.join(model_path, "*.safetensors")))
     if not files:
         raise FileNotFoundError(f"no *.safetensors files in {model_path}")
-    targets = dict(model.named_parameters())
-    targets.update({n: b for n, b in model.named_buffers() if n.endswith(_AWQ_SUFFIXES)})
-    loaded: set[str] = set()
-    unexpected: list[str] = []
-    shards_seen: dict[str, set[str]] = {}
-    for path in files:
-        with safe_open(path, framework="pt", device="cpu") as f:
-            for name in f.keys():
-                if _IGNORED.search(name):
-                    continue
-                stacked = stacked_target(name)
-                if stacked is not None and stacked[0] in targets:
-                    target, shard, shards = stacked
-                    copy_shard(targets[target], f.get_tensor(name), shard, shards, name)
-                    seen = shards_seen.setdefault(target, set())
-                    seen.add(shard)
-                    if seen == set(shards):
-                        loaded.add(target)
-                    continue
-                if name not in targets:
-                    if name != "lm_head.weight":  # tied-embedding checkpoints may still store it
-                        unexpected.append(name)
-                    continue
-                tensor, dst = f.get_tensor(name), targets[name]
-                if tuple(dst.shape) != tuple(tensor.shape):
-                    raise ValueError(f"shape mismatch for {name}: checkpoint {tuple(tensor.shape)} vs model "
-                                     f"{tuple(dst.shape)}")
-                with torch.no_grad():
-                    dst.copy_(tensor.to(dst.dtype))
-                loaded.add(name)
-    if unexpected:
-        logger.warning("ignored %d unexpected checkpoint tensors, e.g. %s", len(unexpected), unexpected[:3])
-    missing = sorted(set(targets) - loaded)
-    if missing:
-        raise RuntimeError(f"{len(missing)} parameters missing from checkpoint, e.g. {missing[:5]}")
+    with contextlib.ExitStack() as stack:
+        handles = [stack.enter_context(safe_open(f, framework="pt", device="cpu")) for f in files]
+        where = {name: h for h in handles for name in h.keys()}  # the last shard wins a duplicate name
+        shape_of = {name: tuple(h.get_slice(name).get_shape()) for name, h in where.items()}
+        targets = model_tensors(model)
+        plans, missing = plan_sources(targets, set(where))
+        if missing:
+            raise RuntimeError(f"the checkpoint in {model_path} lacks {len(missing)} model tensors, "
+                               f"e.g. {sorted(missing)[:5]}")
+        for name, (srcs, axis) in plans.items():
+            got = _stacked_shape([shape_of[s] for s in srcs], axis)
+            if got != tuple(targets[name].shape):
+                detail = ", ".join(f"{s} {shape_of[s]}" for s in srcs)
+                raise ValueError(f"shape mismatch for {name}: model {tuple(targets[name].shape)}, checkpoint {detail}")
+        with torch.no_grad():
+            for name, (srcs, axis) in plans.items():
+                dst = targets[name]
+                parts = [where[s].get_tensor(s) for s in srcs]
+                dst.copy_((parts[0] if len(parts) == 1 else torch.cat(parts, dim=axis)).to(dst.dtype))
+        used = {s for srcs, _ in plans.values() for s in srcs}
+        extra = sorted(n for n in where if n not in used and n != "lm_head.weight" and not n.endswith(_NOT_STATE))
+        if extra:
+            logger.warning("skipped %d checkpoint tensors the model has no place for, e.g. %s", len(extra), extra[:3])

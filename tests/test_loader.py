@@ -72,13 +72,28 @@ def test_quant_config():
             loader.QuantConfig.from_dict(bad)
 
 
-def test_stacked_targets():
-    assert loader.stacked_target("model.layers.3.self_attn.k_proj.qzeros") == (
-        "model.layers.3.self_attn.qkv_proj.qzeros", "k", ("q", "k", "v"))
-    assert loader.stacked_target("model.layers.0.mlp.up_proj.scales") == (
-        "model.layers.0.mlp.gate_up_proj.scales", "up", ("gate", "up"))
-    assert loader.stacked_target("model.layers.0.mlp.experts.3.gate_proj.weight") is None
-    assert loader.stacked_target("model.layers.0.mlp.down_proj.qweight") is None
+def test_fused_sources():
+    """A fused model tensor names its checkpoint parts in stacking order, with the output-feature
+    axis: dim 1 for the AutoAWQ tensors, dim 0 for dense weights and biases."""
+    pre = "model.layers.3.self_attn"
+    assert loader.fused_sources(f"{pre}.qkv_proj.qzeros") == ([f"{pre}.{p}_proj.qzeros" for p in "qkv"], 1)
+    assert loader.fused_sources(f"{pre}.qkv_proj.bias") == ([f"{pre}.{p}_proj.bias" for p in "qkv"], 0)
+    assert loader.fused_sources("model.layers.0.mlp.gate_up_proj.scales") == (
+        ["model.layers.0.mlp.gate_proj.scales", "model.layers.0.mlp.up_proj.scales"], 1)
+    assert loader.fused_sources("model.layers.0.mlp.gate_up_proj.weight")[1] == 0
+    assert loader.fused_sources("model.layers.0.mlp.gate_up_proj.bias") is None
+    assert loader.fused_sources("model.layers.0.mlp.experts.3.gate_up_proj.weight") is None
+    assert loader.fused_sources("model.layers.0.mlp.down_proj.qweight") is None
+
+
+def test_plan_prefers_same_named_tensor():
+    """A checkpoint that already stores the fused tensor fills it directly; a fused tensor with a
+    part absent is reported missing, not half-filled."""
+    t = {"a.self_attn.qkv_proj.weight": torch.zeros(6, 2), "model.layers.0.mlp.gate_up_proj.qweight": torch.zeros(1)}
+    plans, missing = loader.plan_sources(t, {"a.self_attn.qkv_proj.weight", "a.self_attn.q_proj.weight",
+                                             "model.layers.0.mlp.gate_proj.qweight"})
+    assert plans == {"a.self_attn.qkv_proj.weight": (["a.self_attn.qkv_proj.weight"], 0)}
+    assert missing == ["model.layers.0.mlp.gate_up_proj.qweight"]
 
 
 def test_load_fuses_awq_columns(tmp_path):
@@ -101,10 +116,26 @@ def test_load_reports_missing_and_mismatched(tmp_path):
     _checkpoint(tmp_path)
     model = Model(loader.QuantConfig("awq", 4, 128))
     model.model.layers[0].extra = nn.Linear(4, 4)
-    with pytest.raises(RuntimeError, match="missing"):
+    with pytest.raises(RuntimeError, match="lacks 2 model tensors"):
         loader.load_weights(model, str(tmp_path))
     with pytest.raises(FileNotFoundError):
         loader.load_weights(Model(None), str(tmp_path / "nowhere"))
+
+
+def test_load_rejects_shape_mismatch_before_copying(tmp_path):
+    """A checkpoint whose k_proj is wider than the model's qkv leaves room for raises ValueError, and
+    no model tensor has been written."""
+    _checkpoint(tmp_path)
+    model = Model(loader.QuantConfig("awq", 4, 128))
+    model.model.layers[0].self_attn.qkv_proj = linear.make_linear(H, Q + 2 * KV - 8, False, loader.QuantConfig(
+        "awq", 4, 128))
+    with torch.no_grad():
+        for t in loader.model_tensors(model).values():
+            t.zero_()  # W4Linear's AutoAWQ buffers start uninitialised
+    before = {n: t.clone() for n, t in loader.model_tensors(model).items()}
+    with pytest.raises(ValueError, match="qkv_proj"):
+        loader.load_weights(model, str(tmp_path))
+    assert all(torch.equal(before[n], t) for n, t in loader.model_tensors(model).items())
 
 
 @pytest.mark.gpu
