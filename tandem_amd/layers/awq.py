@@ -1,15 +1,17 @@
-"""4-bit AWQ weights (W4A16) on MI355X: load-time repack, decode kernels, prefill path.
+"""The W4A16 linear layer of an AutoAWQ model on MI355X (gfx950), and its load-time helpers.
 
-Drop-in for python/tandem/layers/awq.py (12vivi/tandem): the same AutoAWQ "gemm" buffers, the same
-W4Linear constructor / ``enable_silu_mul`` / ``finalize`` / ``forward`` contract, the same per-GPU
-config tables and ``TANDEM_W4_GEMM`` switch. The kernels are hand-written HIP for gfx950
-(libtandem_w4.so, include/tandem_w4.h); there is no Triton and no CPU path.
+Drop-in for python/tandem/layers/awq.py (12vivi/tandem): a caller builds ``W4Linear`` with the
+constructor it knows, the loader fills the same three buffers, ``enable_silu_mul`` / ``finalize`` /
+``forward`` keep their contract, and the per-GPU tables, ``pick_gemm`` and the ``TANDEM_W4_GEMM``
+switch keep their meaning. Underneath, every kernel is hand-written HIP for gfx950
+(libtandem_w4.so, include/tandem_w4.h): no Triton, no CUDA, no CPU path.
 
-AutoAWQ "gemm" checkpoints store each linear layer as
-    qweight [K, N/8] int32   8 4-bit weights per int32 along the output dim, AWQ nibble order
-    qzeros  [K/G, N/8] int32 zero points, packed the same way
-    scales  [K/G, N]         one scale per group of G = 128 inputs
-and w[k, n] = (q[k, n] - z[k // G, n]) * s[k // G, n].
+The checkpoint side is AutoAWQ's "gemm" packing, which the loader hands over unchanged:
+    qweight  int32 [K, N/8]    output features 8 c .. 8 c + 7 of input k share word (k, c); the
+                               feature 8 c + j sits in nibble AWQ_REVERSE_ORDER[j]
+    qzeros   int32 [K/G, N/8]  the 4-bit zero point of each (group, feature), packed alike
+    scales   fp16  [K/G, N]    the scale of each (group, feature)
+with G = 128 inputs per group, and weight (n, k) = (q - z) * s of its group's zero and scale.
 
 ``finalize`` repacks once, on the GPU, into the tile layout of the MI355X kernels:
     packed [Npad, K/8] int32  (Npad = N rounded up to 16), viewed as [Npad/16][K/128][4 kb][16 r][4 s]:
@@ -40,8 +42,9 @@ from torch import nn
 from tandem_amd.layers import w4_hip
 from tandem_amd.layers.w4_tables import GFX950_DECODE, GFX950_GEMM
 
-# AWQ packs output columns j = 0..7 of an int32 in nibble order [0, 2, 4, 6, 1, 3, 5, 7]: column j
-# lives in nibble REVERSE[j] (python/tandem/layers/awq.py:38-39)
+# Nibble of an AutoAWQ word that holds feature j = 0..7 of its 8: the packer writes features
+# 0, 2, 4, 6, 1, 3, 5, 7 into nibbles 0..7, so feature j is found at this position
+# (python/tandem/layers/awq.py:38-39)
 AWQ_REVERSE_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
 
 
@@ -136,7 +139,7 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 
 
 # Decode kernel per GPU and (N, K, M) / (N, K, M, "silu") for M <= 16, the fastest of
-# `python -m tandem_amd.tune` sweeps on the GPU:
+# `python bench.py tune` sweeps on the GPU:
 #   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4 (with the SwiGLU epilogue too: the
 #                                      reference's SwiGLU gate_up always takes "mma")
 #   ("gemvm", warps_k, unroll, ntile)  the GEMV's arithmetic (exact q - z, scale per group) on the
@@ -226,19 +229,24 @@ FUSED_NORM_CHUNKS = 128
 
 
 class W4Linear(nn.Module):
-    """Linear layer with AWQ 4-bit weights (no bias). Built with the checkpoint's AWQ tensors as
-    buffers (qweight / qzeros / scales, filled by the loader, fused along the output dimension for
-    qkv / gate_up); ``finalize`` repacks them on the GPU into the tile layout
-    (python/tandem/layers/awq.py:206-286).
+    """y = x @ W^T for a bias-free projection whose W is AutoAWQ 4-bit (group 128), x and y fp16.
 
-    ``enable_silu_mul`` (gate_up of a SwiGLU MLP, before ``finalize``): the layer returns
-    silu(gate) * up, [M, out_features / 2], instead of [gate | up]; the kernels apply it in their
-    epilogue (rows reordered as interleave_gate_up)."""
+    Life cycle (python/tandem/layers/awq.py:206-286): constructed empty on the host with the
+    AutoAWQ buffers ``qweight`` / ``qzeros`` / ``scales`` (a fused qkv or gate_up holds its parts
+    side by side along the output features); filled by the loader; moved to the GPU; then
+    ``finalize`` replaces the three buffers by the tile layout (``packed``, ``scales``, ``zeros``) in
+    one repack kernel and picks the device's kernel tables. From then on ``forward`` dispatches by
+    batch size: the (N, K, M) decode table up to M = 16, the M > 16 ladder above, dequantize +
+    torch.matmul where the table says None, the switch is off or x is not 16-byte aligned.
+
+    A SwiGLU MLP's gate_up calls ``enable_silu_mul`` before ``finalize``: the repack then interleaves
+    gate and up rows by 8 and every kernel's epilogue returns silu(gate) * up, [M, out_features / 2]."""
 
     def __init__(self, in_features: int, out_features: int, group: int) -> None:
         super().__init__()
         if group != 128 or in_features % group or out_features % 8:
-            raise ValueError(f"W4Linear: {in_features} x {out_features} with group {group} (group 128 only)")
+            raise ValueError(f"W4Linear({in_features}, {out_features}, group {group}): the kernels take group 128, "
+                             "K a multiple of 128 and N a multiple of 8")
         self.in_features, self.out_features, self.group = in_features, out_features, group
         self.awq_layout = True
         self.silu_mul = False

@@ -1,5 +1,6 @@
-"""Projection layers: nn.Linear, or W4Linear when the checkpoint is AWQ-quantized
-(python/tandem/layers/linear.py:10-31)."""
+"""Projection factory of the decoder layers: a plain nn.Linear for an unquantized checkpoint, a
+W4Linear for an AutoAWQ one. Same two entry points and signatures as
+python/tandem/layers/linear.py:10-31 (make_linear, finalize_quantized)."""
 
 from __future__ import annotations
 
@@ -9,25 +10,26 @@ from torch import nn
 
 
 def make_linear(in_features: int, out_features: int, bias: bool = False, quant: Optional[Any] = None) -> nn.Module:
-    """``quant``: an object with ``group_size`` (tandem's QuantConfig) or None. AWQ layers hold the
-    checkpoint tensors (qweight / qzeros / scales, no dense weight is ever allocated) until
-    ``finalize_quantized``."""
-    if quant is None:
-        return nn.Linear(in_features, out_features, bias=bias)
-    if bias:
-        raise NotImplementedError("quantized projections with a bias")
-    from tandem_amd.layers.awq import W4Linear
+    """The projection module for one weight. ``quant`` is None (dense float weights) or a
+    quantization description with a ``group_size`` attribute (``tandem_amd.loader.QuantConfig``).
+    A W4Linear is created empty: it holds only the AutoAWQ tensors the loader fills, never a dense
+    copy of the weight, and is usable once ``finalize_quantized`` has run. The W4A16 kernels have
+    no bias term, so a biased quantized projection is refused."""
+    if quant is not None:
+        if bias:
+            raise NotImplementedError("quantized projections with a bias")
+        from tandem_amd.layers.awq import W4Linear
 
-    return W4Linear(in_features, out_features, quant.group_size)
+        return W4Linear(in_features, out_features, quant.group_size)
+    return nn.Linear(in_features, out_features, bias=bias)
 
 
 def finalize_quantized(model: nn.Module, device_name: Optional[str] = None) -> int:
-    """After the weights are loaded and on the GPU: repack every quantized layer into its kernel
-    layout and attach this GPU's kernel configs. Returns how many layers."""
-    n = 0
-    for mod in model.modules():
-        finalize = getattr(mod, "finalize", None)
-        if finalize is not None and getattr(mod, "awq_layout", False):
-            finalize(device_name)
-            n += 1
-    return n
+    """Run ``finalize(device_name)`` on every module still holding AutoAWQ tensors (``awq_layout``
+    set): the one-time repack into the kernels' tile layout and the choice of the device's kernel
+    tables. Call it with the weights loaded and the model on its GPU. Returns how many layers it
+    finalized; a second call finds none."""
+    pending = [m for m in model.modules() if getattr(m, "awq_layout", False) and callable(getattr(m, "finalize", None))]
+    for module in pending:
+        module.finalize(device_name)
+    return len(pending)

@@ -25,8 +25,9 @@ from tandem_amd.layers import w4_hip
 def _check(who: str, x: torch.Tensor, weight: torch.Tensor) -> tuple[int, int]:
     if x.dim() != 2 or not x.is_contiguous() or x.dtype != torch.float16 or not x.is_cuda:
         raise RuntimeError(f"{who}: contiguous float16 [M, K] GPU rows expected (got {tuple(x.shape)}, {x.dtype})")
-    if weight.shape != (x.shape[1],) or weight.dtype != torch.float16 or weight.device != x.device:
-        raise RuntimeError(f"{who}: float16 weight [{x.shape[1]}] on x's GPU expected")
+    if (weight.shape != (x.shape[1],) or weight.dtype != torch.float16 or weight.device != x.device
+            or not weight.is_contiguous()):
+        raise RuntimeError(f"{who}: contiguous float16 weight [{x.shape[1]}] on x's GPU expected")
     return x.shape[0], x.shape[1]
 
 
@@ -35,7 +36,14 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tenso
     shape = x.shape
     x2 = x.reshape(-1, shape[-1])
     m, k = _check("rms_norm", x2, weight)
-    y = out if out is not None else torch.empty_like(x2)
+    if out is None:
+        y = torch.empty_like(x2)
+    elif (out.shape != x.shape or out.dtype != torch.float16 or out.device != x.device or not out.is_contiguous()
+          or out.data_ptr() % 16):
+        raise RuntimeError(f"rms_norm: out must be a contiguous 16-byte aligned float16 tensor shaped like x "
+                           f"{tuple(shape)} on x's GPU")
+    else:
+        y = out.view(m, k)
     if m == 0:
         return y.view(shape)
     with torch.cuda.device(x.device):

@@ -193,8 +193,9 @@ class W4Extension:
         if residual is not None and (residual.shape != x.shape or residual.dtype != torch.float16
                                      or not residual.is_contiguous() or residual.device != x.device):
             raise RuntimeError("w4_decode_norm: residual must be a contiguous float16 tensor like x")
-        if norm_weight.shape != (k,) or norm_weight.dtype != torch.float16 or norm_weight.device != x.device:
-            raise RuntimeError(f"w4_decode_norm: float16 norm weight [{k}] on x's GPU expected")
+        if (norm_weight.shape != (k,) or norm_weight.dtype != torch.float16 or norm_weight.device != x.device
+                or not norm_weight.is_contiguous()):
+            raise RuntimeError(f"w4_decode_norm: contiguous float16 norm weight [{k}] on x's GPU expected")
         y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
         r_out = torch.empty_like(x) if residual is not None else None
         with torch.cuda.device(x.device):

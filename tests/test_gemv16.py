@@ -88,3 +88,32 @@ def test_lm_head_shape_through_linear():
         ref = x.float() @ w.float().T
         err = (y.float() - ref).abs()
         assert bool((err <= 1e-2 + 1e-2 * ref.abs()).all()), (m, float(err.max()))
+
+
+@pytest.mark.gpu
+def test_out_and_weight_arguments_are_checked():
+    """A caller's ``out`` of the wrong shape, dtype or layout and a strided norm weight are refused
+    before any launch (a too-small ``out`` would otherwise be written past its end)."""
+    from tandem_amd.layers import norm
+
+    x = torch.randn(2, 1024, device="cuda", dtype=torch.float16)
+    w = torch.randn(64, 1024, device="cuda", dtype=torch.float16)
+    for bad in (torch.empty(2, 32, device="cuda", dtype=torch.float16),
+                torch.empty(2, 64, device="cuda", dtype=torch.float32),
+                torch.empty(64, 2, device="cuda", dtype=torch.float16).t()):
+        with pytest.raises(RuntimeError, match="out must be"):
+            gemv16.gemv(x, w, out=bad)
+    good = torch.empty(2, 64, device="cuda", dtype=torch.float16)
+    assert gemv16.gemv(x, w, out=good) is good
+    nw = torch.ones(2048, device="cuda", dtype=torch.float16)[::2]  # 1024 values, stride 2
+    with pytest.raises(RuntimeError, match="contiguous float16 weight"):
+        norm.rms_norm(x, nw, 1e-6)
+    with pytest.raises(RuntimeError, match="contiguous float16 weight"):
+        norm.fused_add_rms_norm(x.clone(), x.clone(), nw, 1e-6)
+    with pytest.raises(RuntimeError, match="out must be"):
+        norm.rms_norm(x, nw.contiguous(), 1e-6, out=torch.empty(1, 1024, device="cuda", dtype=torch.float16))
+    ext = w4_hip.load()
+    packed = torch.zeros(64, 128, device="cuda", dtype=torch.int32)
+    s = torch.zeros(64, 8, device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="contiguous float16 norm weight"):
+        ext.w4_decode_norm(x, None, nw, 1e-6, packed, s, s, 0, *w4_hip.decode_configs()[0], 0)
