@@ -2,6 +2,8 @@
 
     python bench.py [--steps K] [--warmup W] [--m 1] [--layers 36] [--no-cpu] [--no-detail]
     python bench.py --sweep [--sweep-out FILE]
+    python bench.py tune [--model qwen3-8b] [--ms 1,4,8,16] [--kinds gemv,mma] ...
+    python bench.py prof [--proj gate_up] [--m 1] [--launches 40] ...  |  prof --summarize ...
 
 One step = one decode token's W4A16 linears of the whole Qwen3-8B stack: 36 layers x {qkv
 (K 4096, N 6144), o (4096, 4096), gate_up (4096, 24576), down (12288, 4096)} at M = 1, launched
@@ -13,17 +15,21 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
     B = N K / 2 + N (K/128) 2 + N (K/128) / 2 + 2 M K + 2 M N
 (int4 weights, fp16 scales, int4 zeros, fp16 x and y). The JSON line adds:
   roofline      the dominant kernel (gate_up at the benchmark's M) timed alone with HIP events
-                on its own stream, against MI355X's 8 TB/s HBM peak; `traffic` comes from the
-                committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary when present
-  cpu_baseline  the CPU oracle's dequantize-then-matmul (the reference's fallback restated in
-                numpy) on a bounded sample of the same workload, on this host's cores
+                on its own stream, against MI355X's 8 TB/s HBM peak; beside it the kernel-only
+                time of the committed rocprofv3 summary (profiles/roofline_gate_up_m1.json) and the
+                fraction that gives; `traffic` from that summary's FETCH_SIZE / WRITE_SIZE counters
+  cpu_baseline  the reference's fallback (dequantize the whole weight every call, then one matmul;
+                oracle/torch_fallback.py) in torch on this host's cores, on Qwen3-0.6B's qkv at M = 1
+                (the reference's CPU-runnable config) and on one Qwen3-8B layer at the benchmark's M:
+                fp16 and fp32 products, and the matmul alone on a pre-dequantized weight
   detail        per projection and M in {1, 8, 32}: us/call, GB/s, % of peak, TFLOP/s, the kernel
                 that ran, and at M = 32 the dequantize + torch.matmul comparator
   full_stack    the whole decode step of the linears plus the fp16 lm_head (4096 x 151936, through
                 layers/gemv16.py's table: the HIP fp16 GEMV where it has an entry, else F.linear),
                 M in {1, 8, 32}: us per step and GB/s
-  decode_step   the model's decode step (tandem_amd.model: norms, one-token attention, SwiGLU
-                gate_up, lm_head) replayed from the bucketed HIP graphs of tandem_amd.decode_graph,
+  decode_step   tandem_amd.model's decode step replayed from the bucketed HIP graphs of
+                tandem_amd.decode_graph: norms, SwiGLU gate_up, lm_head and a ONE-TOKEN ATTENTION
+                STAND-IN (no KV cache, no RoPE: the step's launch sequence, not a full model step),
                 M in {1, 8, 32}: us per step, tokens/s, GB/s of the step's weight bytes
 
 --sweep times every single-linear configuration of the benchmark's configs instead (Qwen3-0.6B
@@ -32,13 +38,21 @@ Qwen3-1.7B's four shapes at M in {1, 4, 8}): one JSON line per (shape, M) with u
 TFLOP/s, % of the roofline max(B / 8 TB/s, 2 M N K / 2.5 PFLOP/s), the kernel that ran, and past
 M = 16 the dequantize + torch.matmul comparator. Each shape rotates over enough weight copies
 (>= 1 GB) that every call streams from HBM.
+
+`tune` times every compiled configuration of the chosen kernels per (shape, M) and prints the
+fastest (how layers/w4_tables.py was measured). `prof` is a fixed eager launch sequence for
+hardware-counter runs under rocprofv3, and summarizes their CSV files (see prof_main).
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import json
+import math
 import os
+import statistics
+import subprocess
 import sys
 import time
 
@@ -53,7 +67,7 @@ SWEEP = ((("Qwen3-0.6B", "qkv", 1024, 4096), (1,)),) + tuple(
     (("Qwen3-8B", p, k, n), (1, 4, 8, 16, 24, 32, 64, 256, 1024, 4096)) for p, k, n in QWEN3_8B) + tuple(
     (("Qwen3-1.7B", p, k, n), (1, 4, 8)) for p, k, n in QWEN3_1_7B)
 LM_HEAD = (4096, 151936)  # Qwen3-8B vocabulary x hidden, fp16
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_m1.json")
+ROOFLINE_PROFILE = os.path.join(ROOT, "profiles", "roofline_gate_up_m1.json")
 
 
 def call_bytes(m: int, k: int, n: int) -> int:
@@ -61,41 +75,24 @@ def call_bytes(m: int, k: int, n: int) -> int:
     return n * k // 2 + n * g * 2 + n * g // 2 + 2 * m * k + 2 * m * n
 
 
-def parse() -> argparse.Namespace:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--m", type=int, default=1, help="tokens per call (decode batch)")
-    ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-detail", action="store_true", help="skip the per-projection sweep")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
-    ap.add_argument("--sweep", action="store_true", help="time every (shape, M) of the configs; JSON line each")
-    ap.add_argument("--sweep-out", default="", help="also append the sweep's JSON lines to this file")
-    ap.add_argument("--step-only", action="store_true",
-                    help="only the decode_step section (for profiling the whole step); prints its JSON")
-    return ap.parse_args()
+# ------------------------------------------------------------------------------ shared helpers
+def random_linear(torch, awq, k: int, n: int, dev, g, silu: bool = False):
+    """One W4Linear with random AutoAWQ weights (uniform int4 q and z, fp16 scales in [0.001, 0.02]),
+    repacked by the product's finalize."""
+    lin = awq.W4Linear(k, n, 128).to(dev)
+    lin.qweight.copy_(torch.randint(-2**31, 2**31 - 1, lin.qweight.shape, device=dev, dtype=torch.int32, generator=g))
+    lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32, generator=g))
+    lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
+    if silu:
+        lin.enable_silu_mul()
+    lin.finalize(torch.cuda.get_device_name(dev))
+    return lin
 
 
 def make_layers(torch, awq, n_layers: int, dev, seed: int = 0):
-    """Random AutoAWQ weights (uniform int4 q and z, fp16 scales in [0.001, 0.02]) for every
-    projection of every layer, repacked by the product's W4Linear.finalize."""
+    """Every projection of every layer with its own random weights."""
     g = torch.Generator(device=dev).manual_seed(seed)
-    name = torch.cuda.get_device_name(dev)
-    layers = []
-    for _ in range(n_layers):
-        layer = {}
-        for proj, k, n in QWEN3_8B:
-            lin = awq.W4Linear(k, n, 128).to(dev)
-            lin.qweight.copy_(torch.randint(-2**31, 2**31 - 1, lin.qweight.shape, device=dev, dtype=torch.int32,
-                                            generator=g))
-            lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32,
-                                           generator=g))
-            lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
-            lin.finalize(name)
-            layer[proj] = lin
-        layers.append(layer)
+    layers = [{proj: random_linear(torch, awq, k, n, dev, g) for proj, k, n in QWEN3_8B} for _ in range(n_layers)]
     torch.cuda.synchronize()
     return layers
 
@@ -127,8 +124,7 @@ def time_graph(torch, graph, stream, reps: int) -> float:
 def kernel_of(awq, lin, m: int) -> str:
     """Which kernel W4Linear.forward runs for M (the same lookups as the forward)."""
     if m <= 16:
-        key = (lin.out_features, lin.in_features, m)
-        kind = (lin.kernels.get((*key, "silu")) if lin.silu_mul else None) or lin.kernels.get(key, awq.DEFAULT_KERNEL)
+        kind = lin.decode_entry(m)
         if kind[0] in ("gemv", "gemvm") and m > 4:
             kind = awq.DEFAULT_KERNEL
         return f"{kind[0]}{tuple(kind[1:])}"
@@ -139,17 +135,7 @@ def kernel_of(awq, lin, m: int) -> str:
     return f"mma{tuple(cfg[1:])}" if cfg[0] == "mma" else f"gemm{cfg}"
 
 
-def random_linear(torch, awq, k: int, n: int, dev, g):
-    """One W4Linear with random AutoAWQ weights (uniform int4 q and z, fp16 scales in [0.001, 0.02]),
-    repacked by the product's finalize."""
-    lin = awq.W4Linear(k, n, 128).to(dev)
-    lin.qweight.copy_(torch.randint(-2**31, 2**31 - 1, lin.qweight.shape, device=dev, dtype=torch.int32, generator=g))
-    lin.qzeros.copy_(torch.randint(-2**31, 2**31 - 1, lin.qzeros.shape, device=dev, dtype=torch.int32, generator=g))
-    lin.scales.copy_((torch.rand(lin.scales.shape, device=dev, generator=g) * 0.019 + 0.001).half())
-    lin.finalize(torch.cuda.get_device_name(dev))
-    return lin
-
-
+# ------------------------------------------------------------------------------------ sweep
 def sweep(torch, awq, dev, stream, out_path: str) -> int:
     """Per (shape, M): us/call over C weight copies (>= 1 GB in all) replayed from one HIP graph."""
     g = torch.Generator(device=dev).manual_seed(0)
@@ -186,49 +172,78 @@ def sweep(torch, awq, dev, stream, out_path: str) -> int:
     return 0
 
 
-def cpu_baseline(budget_s: float, m: int) -> dict:
-    """The CPU oracle (numpy) dequantize-then-matmul on whole Qwen3-8B projections at M, repeated
-    until ~budget_s seconds; GB/s of the same algorithmic bytes as the GPU figure."""
+# ----------------------------------------------------------------------------- CPU baseline
+def _cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        return next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), "")
+    except (OSError, subprocess.SubprocessError):
+        return ""
+
+
+def cpu_baseline(m: int) -> dict:
+    """The reference's fallback restated in torch (oracle/torch_fallback.py: unpack + fp16 dequant of the
+    whole weight every call, then one product; python/tandem/layers/awq.py:282-286) on this host:
+    Qwen3-0.6B's qkv (K 1024, N 4096) at M = 1 and one Qwen3-8B layer's four projections at M, each
+    with the product in fp16 and in fp32 and the pre-dequantized matmul alone; 3 warm-ups, then the
+    median of 10 timed calls. `value` is the 8B layer's fp16 variant in GB/s of the same
+    algorithmic bytes as the GPU figure."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    import torch
 
     from oracle import awq_oracle as o
+    from oracle import torch_fallback as tf
 
     cores = len(os.sched_getaffinity(0))
-    threads = max(1, min(cores, 16))
-    data = []
-    for i, (proj, k, n) in enumerate(QWEN3_8B):
-        qw, qz, s, _, _ = o.random_awq(k, n, seed=1000 + i)
-        x = np.random.default_rng(i).standard_normal((m, k)).astype(np.float16)
-        data.append((proj, k, n, qw, qz, s, x))
-    total_bytes, done, t_total = 0, 0, 0.0
-    with threadpool_limits(limits=threads):
-        t0 = time.perf_counter()
-        while True:
-            for proj, k, n, qw, qz, s, x in data:
-                t = time.perf_counter()
-                o.dequant_then_linear(x, qw, qz, s)
-                t_total += time.perf_counter() - t
-                total_bytes += call_bytes(m, k, n)
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-    model = ""
-    try:
-        with open("/proc/cpuinfo", encoding="utf-8") as f:
-            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
-    except OSError:
-        pass
-    return {"value": round(total_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{done} x one Qwen3-8B layer's 4 projections at M={m} (qkv, o, gate_up, down): numpy "
-                      f"AWQ unpack + fp16 dequant + float32 BLAS matmul per call, BLAS on {threads} threads "
-                      f"(dequant single-threaded); {t_total:.1f} s; host {model} ({cores} cores visible)",
-            "ms_per_layer": round(t_total / done * 1e3, 2)}
+    threads = min(cores, 16)  # one GPU's share of the box's host cores
+    torch.set_num_threads(threads)
+
+    def median_s(fn) -> float:
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(10):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    def workload(shapes, mm, seed):
+        data = []
+        for i, (k, n) in enumerate(shapes):
+            qw, qz, s, _, _ = o.random_awq(k, n, seed=seed + i)
+            x = torch.from_numpy(np.random.default_rng(seed + i).standard_normal((mm, k)).astype(np.float16))
+            data.append((x, torch.from_numpy(qw), torch.from_numpy(qz), torch.from_numpy(s)))
+        return data
+
+    t_start = time.perf_counter()
+    res = {}
+    for label, shapes, mm in (("qwen3_0.6b_qkv_m1", [(1024, 4096)], 1),
+                              (f"qwen3_8b_layer_m{m}", [(k, n) for _, k, n in QWEN3_8B], m)):
+        data = workload(shapes, mm, seed=1000)
+        b = sum(call_bytes(mm, k, n) for k, n in shapes)
+        rec = {}
+        for variant, dt in (("fp16", torch.float16), ("fp32", torch.float32)):
+            sec = median_s(lambda: [tf.fallback_linear(x, qw, qz, s, dt) for x, qw, qz, s in data])
+            rec[variant] = {"ms": round(sec * 1e3, 2), "GBps": round(b / sec / 1e9, 3)}
+        pre = [(x, tf.dequant_kn(qw, qz, s)) for x, qw, qz, s in data]
+        sec = median_s(lambda: [x @ w for x, w in pre])
+        rec["matmul_only_predequantized_fp16"] = {"ms": round(sec * 1e3, 3), "GBps": round(b / sec / 1e9, 3)}
+        res[label] = rec
+    main = res[f"qwen3_8b_layer_m{m}"]["fp16"]
+    return {"value": main["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the reference's fallback (AWQ unpack + fp16 dequant of the whole weight every call, then "
+                      f"one matmul) in torch on {threads} threads: one Qwen3-8B layer's qkv, o, gate_up and down at "
+                      f"M={m} (value: fp16 product) and Qwen3-0.6B qkv at M=1; 3 warm-ups + median of 10 calls "
+                      f"each; host {_cpu_model()} ({cores} cores visible); "
+                      f"{time.perf_counter() - t_start:.1f} s in all",
+            "ms_per_call": main["ms"], "variants": res}
 
 
+# ------------------------------------------------------------------------------ decode step
 def decode_step(torch, dev) -> dict:
-    """The whole Qwen3-8B decode step of tandem_amd.model (embedding, 36 x {add + RMSNorm, qkv,
-    one-token attention, o, add + RMSNorm, gate_up with SwiGLU, down}, final add + RMSNorm, fp16
+    """tandem_amd.model's Qwen3-8B decode step (embedding, 36 x {add + RMSNorm, qkv, ONE-TOKEN
+    ATTENTION STAND-IN, o, add + RMSNorm, gate_up with SwiGLU, down}, final add + RMSNorm, fp16
     lm_head) replayed from tandem_amd.decode_graph's bucket graphs, random AWQ weights."""
     from tandem_amd import decode_graph, model as tmodel
     from tandem_amd.loader import QuantConfig
@@ -242,7 +257,7 @@ def decode_step(torch, dev) -> dict:
     runner = decode_graph.DecodeGraphRunner(mdl, max_bs=32, device=dev)
     h, i, v = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     qkv_n = (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
-    out = {}
+    out = {"what": "linears + norms + lm_head around a one-token attention stand-in (no KV cache, no RoPE)"}
     for bs in (1, 8, 32):
         runner.run(list(range(bs)))
         graph = runner.graphs[bs]
@@ -265,8 +280,33 @@ def decode_step(torch, dev) -> dict:
     return out
 
 
-def main() -> int:
-    a = parse()
+# -------------------------------------------------------------------------------- headline
+def parse(argv=None) -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--m", type=int, default=1, help="tokens per call (decode batch)")
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-detail", action="store_true", help="skip the per-projection sweep")
+    ap.add_argument("--sweep", action="store_true", help="time every (shape, M) of the configs; JSON line each")
+    ap.add_argument("--sweep-out", default="", help="also append the sweep's JSON lines to this file")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the decode_step section (for profiling the whole step); prints its JSON")
+    return ap.parse_args(argv)
+
+
+def roofline_profile(m: int) -> dict:
+    """The committed rocprofv3 summary of the dominant kernel (kernel-only time, HBM counters)."""
+    if m != 1 or not os.path.exists(ROOFLINE_PROFILE):
+        return {}
+    with open(ROOFLINE_PROFILE, encoding="utf-8") as f:
+        return json.load(f)
+
+
+def main(argv=None) -> int:
+    a = parse(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {a.gpus} is not supported (the W4A16 linear runs on one GPU's "
               "share of the weights; sharding splits N or K across GPUs outside this op)", file=sys.stderr)
@@ -300,8 +340,9 @@ def main() -> int:
     step_graph = graph_of(torch, step, stream)
     step_bytes = a.layers * sum(call_bytes(m, k, n) for _, k, n in QWEN3_8B)
     step_flops = a.layers * sum(2 * m * k * n for _, k, n in QWEN3_8B)
-    for _ in range(a.warmup):
-        step_graph.replay()
+    with torch.cuda.stream(stream):
+        for _ in range(a.warmup):
+            step_graph.replay()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
@@ -318,14 +359,15 @@ def main() -> int:
     gate_s = time_graph(torch, gate_graph, stream, reps=max(10, a.steps // 4)) / a.layers
     gate_bytes = call_bytes(m, 4096, 24576)
     achieved = gate_bytes / gate_s / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE) and m == 1:
-        with open(TRAFFIC_FILE, encoding="utf-8") as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    prof = roofline_profile(m)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": prof.get("hbm_bytes_per_launch"),
                 "kernel": f"gate_up (K 4096, N 24576) M={m}: {kernel_of(awq, layers[0]['gate_up'], m)}",
                 "us_per_launch": round(gate_s * 1e6, 3), "algorithmic_bytes_per_launch": gate_bytes}
+    if prof.get("kernel_us"):
+        roofline["profile_kernel_us"] = prof["kernel_us"]
+        roofline["profile_frac"] = round(gate_bytes / prof["kernel_us"] / 1e3 / HBM_PEAK_GBS, 4)
+        roofline["profile"] = os.path.relpath(ROOFLINE_PROFILE, ROOT)
     del gate_graph
 
     detail = {}
@@ -338,7 +380,8 @@ def main() -> int:
                 us = time_graph(torch, g, stream, reps=20) / a.layers * 1e6
                 del g
                 b, f = call_bytes(mm, k, n), 2 * mm * k * n
-                rec = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1),
+                rec = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                       "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1),
                        "TFLOPs": round(f / us / 1e6, 2), "kernel": kernel_of(awq, layers[0][proj], mm)}
                 if mm == 32:  # the dequantize-then-fp16-GEMM comparator (HIP dequant + torch.matmul)
                     dg = graph_of(torch, lambda: [layer[proj]._dense(xd[k]) for layer in layers[:8]], stream)
@@ -371,14 +414,13 @@ def main() -> int:
             b = a.layers * sum(call_bytes(mm, k, n) for _, k, n in QWEN3_8B) + 2 * hn * hk + 2 * mm * (hk + hn)
             full[f"m{mm}"] = {"us_per_step": round(us, 1), "GBps": round(b / us / 1e3, 1),
                               "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1), "step_bytes": b,
-                              "lm_head": "gemv16" if table.get((hn, hk, gemv16.m_bucket(mm))) and mm <= 8
-                              else "F.linear"}
+                              "lm_head": "gemv16" if gemv16.entry(xd[4096], head, table) else "F.linear"}
         del head
         torch.cuda.synchronize()
 
     step = {} if a.no_detail else decode_step(torch, dev)
 
-    cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds, m)
+    cpu = None if a.no_cpu else cpu_baseline(m)
     line = {
         "metric": "W4A16 us/call + achieved HBM GB/s (% peak), Qwen3-8B shapes, M=1/8/32",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -397,5 +439,360 @@ def main() -> int:
     return 0
 
 
+# ------------------------------------------------------------------------------------- tune
+TUNE_MODELS = {
+    "qwen3-8b": {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096),
+                 "lm_head": (4096, 151936)},
+    "qwen3-1.7b": {"qkv": (2048, 4096), "o": (2048, 2048), "gate_up": (2048, 12288), "down": (6144, 2048),
+                   "lm_head": (2048, 151936)},
+    "qwen3-0.6b": {"qkv": (1024, 4096), "lm_head": (1024, 151936)},
+}
+DENSE = ("lm_head",)  # fp16 projections (kinds dense16 / torch16); the others are W4A16
+
+
+def tune_main(argv=None) -> int:
+    """Configuration sweep of the W4A16 kernels, the counterpart of the reference's
+    benchmarks/bench_w4.py and bench_w4_gemm.py, which produced its per-GPU tables:
+
+        python bench.py tune --model qwen3-8b --ms 1,4,8,16 --kinds gemv,mma [--out sweep.jsonl]
+        python bench.py tune --model qwen3-8b --ms 24,32,64,256 --kinds gemm
+        python bench.py tune --model qwen3-8b --projs lm_head --ms 1,2,4,8 --kinds dense16,torch16
+
+    For each projection shape and M, every compiled configuration of each kernel is timed the way the
+    reference timed them (benchmarks/bench_gemv.py:35-56): one HIP graph replays `rounds` passes over
+    `copies` weight copies whose total size (>= --footprint-mb, default 1 GB) is far beyond the 256 MB
+    Infinity Cache, so each call streams its weights from HBM. One JSON record per (shape, M) gives
+    us/call and GB/s of the best config of each kind and of every config."""
+    import torch
+
+    from tandem_amd.layers import w4_hip
+
+    ap = argparse.ArgumentParser(prog="bench.py tune", description=tune_main.__doc__.split("\n\n")[0])
+    ap.add_argument("--model", default="qwen3-8b", choices=sorted(TUNE_MODELS))
+    ap.add_argument("--projs", default="", help="comma list of projections (default: all)")
+    ap.add_argument("--ms", default="1,4,8,16")
+    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, gemvn, mma, mmak, mmap, gemm, dense")
+    ap.add_argument("--splits", default="0,1,2,4,8")
+    ap.add_argument("--per-cu", default="1,2,3,4", help="workgroups per CU of the persistent mma (kind mmap)")
+    ap.add_argument("--act", action="store_true", help="time the SwiGLU epilogue (gate_up only)")
+    ap.add_argument("--footprint-mb", type=float, default=1024.0)
+    ap.add_argument("--out", default="")
+    a = ap.parse_args(argv)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    ext = w4_hip.load()
+    gen = torch.Generator(device=dev).manual_seed(0)
+    stream = torch.cuda.Stream(dev)
+    kinds = a.kinds.split(",")
+    buf, locks = w4_hip.workspace(dev)
+    out = open(a.out, "a", encoding="utf-8") if a.out else None
+
+    def time_us(calls, rounds: int = 10, reps: int = 5) -> float:
+        """Microseconds per call: a HIP graph of `rounds` passes over `calls`, replayed `reps` times."""
+        graph = graph_of(torch, lambda: [c() for _ in range(rounds) for c in calls], stream)
+        return time_graph(torch, graph, stream, reps) * 1e6 / (rounds * len(calls))
+
+    def random_weights(k: int, n: int):
+        """Uniform random nibbles straight in the tile layout, fp16 scales in [0.001, 0.02], integer zeros."""
+        packed = torch.randint(-2**31, 2**31 - 1, (w4_hip.padded_rows(n), k // 8), dtype=torch.int32, device=dev,
+                               generator=gen)
+        scales = (torch.rand(n, k // 128, device=dev, generator=gen) * 0.019 + 0.001).half()
+        zeros = torch.randint(0, 16, (n, k // 128), device=dev, generator=gen).half()
+        return packed, scales, zeros
+
+    def emit(proj: str, k: int, n: int, m: int, act: int, copies: int, res: dict, b: int) -> None:
+        if not res:
+            return
+        best = min(res, key=res.get)
+        rec = {"model": a.model, "proj": proj, "k": k, "n": n, "m": m, "act": act, "copies": copies,
+               "best": list(best), "us": round(res[best], 3), "GBps": round(b / res[best] / 1e3, 1),
+               "pct_hbm_peak": round(b / res[best] / 1e3 / HBM_PEAK_GBS * 100, 2),
+               "TFLOPs": round(2 * m * k * n / res[best] / 1e6, 2),
+               "best_per_kind": {kd: min((v, list(c)) for c, v in res.items() if c[0] == kd)
+                                 for kd in {c[0] for c in res}},
+               "all": {"/".join(map(str, c)): round(v, 2) for c, v in sorted(res.items(), key=lambda kv: kv[1])}}
+        print(json.dumps(rec), flush=True)
+        if out:
+            out.write(json.dumps(rec) + "\n")
+
+    def attempt(res: dict, key: tuple, calls, rounds: int = 10) -> None:
+        try:
+            res[key] = time_us(calls, rounds)
+        except RuntimeError:  # a configuration the host checks refuse for this shape
+            pass
+
+    for proj, (k, n) in TUNE_MODELS[a.model].items():
+        if (a.projs and proj not in a.projs.split(",")) or (a.act and proj != "gate_up"):
+            continue
+        act = int(a.act)
+        if (proj in DENSE) != any(kd in kinds for kd in ("dense16", "torch16")):
+            continue
+        if proj in DENSE:  # fp16 weights [N, K]: the kernel of layers/gemv16.py against F.linear
+            from tandem_amd.layers import gemv16
+
+            wbytes = 2 * n * k
+            copies = max(1, math.ceil(a.footprint_mb * 1e6 / wbytes))
+            wd = [(torch.randn(n, k, device=dev, generator=gen) * 0.02).half() for _ in range(copies)]
+            for m in (int(v) for v in a.ms.split(",")):
+                x = torch.randn(m, k, device=dev, dtype=torch.float16)
+                res = {}
+                if "dense16" in kinds:
+                    for cfg in w4_hip.gemv_f16_configs():
+                        attempt(res, ("dense16", *cfg), [lambda w=w, c=cfg: gemv16.gemv(x, w, *c) for w in wd], 3)
+                if "torch16" in kinds:
+                    attempt(res, ("torch16",), [lambda w=w: torch.nn.functional.linear(x, w) for w in wd], 3)
+                emit(proj, k, n, m, 0, copies, res, wbytes + 2 * m * k + 2 * m * n)
+            del wd
+            torch.cuda.empty_cache()
+            continue
+        copies = max(2, math.ceil(a.footprint_mb * 1e6 / call_bytes(0, k, n)))
+        ws = [random_weights(k, n) for _ in range(copies)]
+        for m in (int(v) for v in a.ms.split(",")):
+            x = torch.randn(m, k, device=dev, dtype=torch.float16)
+            res = {}
+            for cfg in w4_hip.decode_configs():
+                if "gemv" in kinds and m <= 4:
+                    attempt(res, ("gemv", *cfg), [lambda w=w, c=cfg: ext.w4_gemv(x, *w, *c, act) for w in ws])
+                if "gemvn" in kinds and m <= 4:  # the GEMV with the add + RMSNorm prologue (tw4_decode_norm)
+                    r = torch.randn(m, k, device=dev, dtype=torch.float16)
+                    nw = (torch.rand(k, device=dev) + 0.5).half()
+                    attempt(res, ("gemvn", *cfg),
+                            [lambda w=w, c=cfg: ext.w4_decode_norm(x, r, nw, 1e-6, *w, 0, *c, act) for w in ws])
+                if "gemvm" in kinds and m <= 4:
+                    attempt(res, ("gemvm", *cfg), [lambda w=w, c=cfg: ext.w4_gemv_mfma(x, *w, *c, act) for w in ws])
+                if "mma" in kinds and m <= 64:
+                    attempt(res, ("mma", *cfg), [lambda w=w, c=cfg: ext.w4_mma(x, *w, *c, act) for w in ws])
+                if "mmap" in kinds and m <= 16:
+                    for pc in (int(v) for v in a.per_cu.split(",")):
+                        attempt(res, ("mmap", *cfg, pc),
+                                [lambda w=w, c=cfg, q=pc: ext.w4_mma_persist(x, *w, *c, q, act) for w in ws])
+                if "mmak" in kinds and m <= 16:
+                    for sp in (int(v) for v in a.splits.split(",")):
+                        if 2 <= sp <= k // 128:
+                            attempt(res, ("mmak", *cfg, sp),
+                                    [lambda w=w, c=cfg, s=sp: ext.w4_mma_splitk(x, *w, buf, locks, *c, s, act)
+                                     for w in ws])
+            if "gemm" in kinds:
+                for cfg in w4_hip.gemm_configs():
+                    for sp in (int(v) for v in a.splits.split(",")):
+                        if sp <= (k // 128 + cfg[3] - 1) // cfg[3]:
+                            attempt(res, ("gemm", *cfg, sp),
+                                    [lambda w=w, c=cfg, s=sp: ext.w4_gemm(x, *w, buf, locks, *c, s, act) for w in ws],
+                                    5)
+            if "dense" in kinds:  # HIP dequantize + torch.matmul, the unfused comparator
+                from tandem_amd.layers import awq
+
+                def dense(w):
+                    y = torch.nn.functional.linear(x, awq.w4_dequant(*w, deinterleave=bool(act)))
+                    return awq.silu_and_mul(y) if act else y
+
+                attempt(res, ("dense",), [lambda w=w: dense(w) for w in ws[:8]], 3)
+            emit(proj, k, n, m, act, copies, res, call_bytes(m, k, n))
+        del ws
+        torch.cuda.empty_cache()
+    if out:
+        out.close()
+    return 0
+
+
+# ------------------------------------------------------------------------------------- prof
+PROF_SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+COPY_KERNEL_HINT = ("copybuffer",)  # the HIP runtime's device-to-device copy (torch copy_ of one dtype)
+LOAD_TIME_KERNELS = ("repack",)     # finalize's kernels: never the kernel a profile is about
+
+
+def prof_main(argv=None) -> int:
+    """A fixed, eager sequence of kernel launches for hardware-counter runs under rocprofv3, and the
+    summaries of those runs.
+
+        python bench.py prof [--proj gate_up] [--m 1] [--launches 40] [--copy-mib 256]
+
+    Launches, in order: `copies` torch copies of a --copy-mib MiB float16 buffer (a plain device copy
+    of known size: it reads and writes exactly that many bytes, which calibrates FETCH_SIZE and
+    WRITE_SIZE), then --launches calls of W4Linear.forward for one Qwen3-8B projection at M, rotating
+    over enough weight copies (>= 1 GB) that every call streams its weights from HBM. --read-gb adds a
+    streaming calibration before the copies: one torch sum over a --read-gb GB float16 buffer (reads
+    only), the plain-read ceiling the decode kernels are held against. A counter run reads, per
+    dispatch, the HBM bytes each kernel moved:
+
+        rocprofv3 --pmc FETCH_SIZE -d <dir> -o run --output-format csv -- python3 bench.py prof
+        rocprofv3 --pmc WRITE_SIZE -d <dir> -o run --output-format csv -- python3 bench.py prof
+        python bench.py prof --summarize <fetch counter_collection.csv> <write counter_collection.csv>
+
+    The summary's kernel is the one the command targets: a tw4 kernel with exactly --launches
+    dispatches, never a load-time repack. The same launches give the GEMM's matrix-core utilisation
+    (M > 16; --cfg forces one GEMM configuration, mt,nt,warps_n,warps_k,stages,splits, in place of
+    the table's, to compare tile and split-K choices on the same shape):
+
+        rocprofv3 --kernel-trace --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_F16 -d <dir> -o run \\
+            --output-format csv -- python3 bench.py prof --proj gate_up --m 32 [--cfg 2,1,4,2,2,1]
+        python bench.py prof --proj gate_up --m 32 --summarize-mfma <counter_collection.csv>
+
+    MfmaUtil is rocprofiler's derived counter: the SIMDs' summed SQ_VALU_MFMA_BUSY_CYCLES over
+    GRBM_GUI_ACTIVE x the number of SIMDs, in percent. SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 is the fp16
+    matrix-core work issued, which against 2 M N K shows the padding of the token tiles."""
+    ap = argparse.ArgumentParser(prog="bench.py prof", description=prof_main.__doc__.split("\n\n")[0])
+    ap.add_argument("--proj", default="gate_up", choices=sorted(PROF_SHAPES))
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--launches", type=int, default=40)
+    ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--read-gb", type=float, default=0.0, help="plain-read calibration size (0: none)")
+    ap.add_argument("--silu", action="store_true", help="gate_up with the SwiGLU epilogue")
+    ap.add_argument("--cfg", default="", help="GEMM config mt,nt,warps_n,warps_k,stages,splits for every M > 16")
+    ap.add_argument("--summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--summarize-mfma", metavar="COUNTER_CSV")
+    a = ap.parse_args(argv)
+    k, n = PROF_SHAPES[a.proj]
+    if a.summarize_mfma:
+        print(json.dumps(summarize_mfma(a.summarize_mfma, a.m, n, k), indent=1))
+        return 0
+    if a.summarize:
+        alg = call_bytes(a.m, k, n) - (a.m * n if a.silu else 0)
+        print(json.dumps(summarize_traffic(*a.summarize, a.copy_mib, a.copies, a.launches, alg), indent=1))
+        return 0
+    return prof_run(a)
+
+
+def prof_run(a: argparse.Namespace) -> int:
+    import torch
+
+    from tandem_amd.layers import awq, w4_hip
+
+    if not torch.cuda.is_available():
+        print("bench.py prof needs the GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    w4_hip.load()
+    if a.read_gb > 0:
+        big = torch.ones(int(a.read_gb * 1e9) // 2, device=dev, dtype=torch.float16)
+        for _ in range(3):
+            big.sum(dtype=torch.float32)
+        torch.cuda.synchronize()
+        del big
+    src = torch.ones(a.copy_mib << 19, device=dev, dtype=torch.float16)
+    dst = torch.empty_like(src)
+    for _ in range(a.copies):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+    k, n = PROF_SHAPES[a.proj]
+    g = torch.Generator(device=dev).manual_seed(0)
+    copies = max(2, -(-(1 << 30) // (n * k // 2)))
+    layers = []
+    for _ in range(copies):
+        lin = random_linear(torch, awq, k, n, dev, g, silu=a.silu and a.proj == "gate_up")
+        if a.cfg:  # a per-layer copy: the module-level table is shared by every W4Linear
+            key = (n, k) + (("silu",) if lin.silu_mul else ())
+            lin.gemm_kernels = {**lin.gemm_kernels, key: ((1 << 30, tuple(int(v) for v in a.cfg.split(","))),)}
+        layers.append(lin)
+    x = torch.randn(a.m, k, device=dev, dtype=torch.float16)
+    torch.cuda.synchronize()
+    for i in range(a.launches):
+        layers[i % copies](x)
+    torch.cuda.synchronize()
+    print(f"prof: {a.copies} copies of {a.copy_mib} MiB, {a.launches} x {a.proj} (K {k}, N {n}) M={a.m} "
+          f"over {copies} weight copies ({kernel_of(awq, layers[0], a.m)}), read calibration {a.read_gb} GB",
+          flush=True)
+    return 0
+
+
+def _per_kernel(path: str, counter: str) -> dict[str, list[tuple[int, float]]]:
+    """counter_collection.csv -> {kernel name: [(dispatch id, counter value), ...] in dispatch order}."""
+    out: dict[str, list[tuple[int, float]]] = {}
+    with open(path, newline="", encoding="utf-8") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") == counter:
+                out.setdefault(row["Kernel_Name"], []).append((int(row["Dispatch_Id"]), float(row["Counter_Value"])))
+    for v in out.values():
+        v.sort()
+    return out
+
+
+def _calibration(per_kernel: dict[str, list[tuple[int, float]]], copies: int) -> tuple[str, list[float]]:
+    """The calibration copies: the first `copies` dispatches of the run that are copy kernels."""
+    first = sorted((d, name, val) for name, v in per_kernel.items() for d, val in v
+                   if any(h in name.lower() for h in COPY_KERNEL_HINT) and "tw4" not in name)[:copies]
+    if len(first) < copies or len({name for _, name, _ in first}) != 1:
+        raise SystemExit("the counter file does not start with the calibration copies")
+    return first[0][1], [val for _, _, val in first]
+
+
+def target_kernel(names_to_dispatches: dict[str, int], launches: int) -> str | None:
+    """The kernel a prof command targets: a tw4 kernel with exactly `launches` dispatches that is not a
+    load-time kernel; else the most-dispatched such kernel."""
+    cands = {nm: d for nm, d in names_to_dispatches.items()
+             if "tw4" in nm and not any(t in nm for t in LOAD_TIME_KERNELS)}
+    exact = [nm for nm, d in cands.items() if d == launches]
+    if exact:
+        return exact[0]
+    return max(cands, key=cands.get) if cands else None
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str, copy_mib: int, copies: int, launches: int,
+                      algorithmic_bytes: int | None) -> dict:
+    """Average FETCH_SIZE / WRITE_SIZE (KiB) per dispatch of each tw4 kernel, and its HBM bytes per
+    launch: each counter scaled by known bytes / what the counter reads for the calibration copy."""
+    fetch, write = _per_kernel(fetch_csv, "FETCH_SIZE"), _per_kernel(write_csv, "WRITE_SIZE")
+    copy_name, cf = _calibration(fetch, copies)
+    _, cw = _calibration(write, copies)
+    known_kib = copy_mib * 1024.0
+    f_fetch, f_write = known_kib / (sum(cf) / len(cf)), known_kib / (sum(cw) / len(cw))
+    rows = {}
+    for name, v in fetch.items():
+        if "tw4" not in name:
+            continue
+        fk = sum(val for _, val in v) / len(v)
+        w = write.get(name, [])
+        wk = sum(val for _, val in w) / len(w) if w else 0.0
+        rows[name] = {"dispatches": len(v), "FETCH_SIZE_KiB": round(fk, 1), "WRITE_SIZE_KiB": round(wk, 1),
+                      "hbm_bytes": round((fk * f_fetch + wk * f_write) * 1024)}
+    rec = {"copy_kernel": copy_name, "copy_MiB": copy_mib, "copy_FETCH_SIZE_KiB": [round(c, 1) for c in cf],
+           "copy_WRITE_SIZE_KiB": [round(c, 1) for c in cw], "fetch_factor": round(f_fetch, 4),
+           "write_factor": round(f_write, 4), "kernels": rows}
+    main_k = target_kernel({nm: r["dispatches"] for nm, r in rows.items()}, launches)
+    if main_k:
+        rec["kernel"] = main_k
+        rec["hbm_bytes_per_launch"] = rows[main_k]["hbm_bytes"]
+        if algorithmic_bytes:
+            rec["algorithmic_bytes_per_launch"] = algorithmic_bytes
+            rec["traffic_over_algorithmic"] = round(rows[main_k]["hbm_bytes"] / algorithmic_bytes, 4)
+    return rec
+
+
+def summarize_mfma(path: str, m: int, n: int, k: int) -> dict:
+    """Per tw4 kernel: average MfmaUtil (%) and fp16 MFMA work per dispatch (SQ_INSTS_VALU_MFMA_MOPS_F16
+    x 512 flops) against the algorithmic 2 M N K, plus the dispatch's duration where the file has
+    timestamps (a --kernel-trace run of the same command)."""
+    util, mops = _per_kernel(path, "MfmaUtil"), _per_kernel(path, "SQ_INSTS_VALU_MFMA_MOPS_F16")
+    dur: dict[str, list[float]] = {}
+    with open(path, newline="", encoding="utf-8") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") == "MfmaUtil" and row.get("Start_Timestamp") and row.get("End_Timestamp"):
+                dur.setdefault(row["Kernel_Name"], []).append(
+                    (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    alg = 2 * m * n * k
+    rows = {}
+    for name, v in util.items():
+        if "tw4" not in name or any(t in name for t in LOAD_TIME_KERNELS):
+            continue
+        mv = [val for _, val in mops.get(name, [])]
+        flops = 512 * sum(mv) / len(mv) if mv else None
+        row = {"dispatches": len(v), "MfmaUtil_pct": round(sum(val for _, val in v) / len(v), 2),
+               "mfma_flops": flops, "algorithmic_flops": alg,
+               "mfma_over_algorithmic": round(flops / alg, 4) if flops else None}
+        if dur.get(name):
+            us = sum(dur[name]) / len(dur[name])
+            row["us_under_counters"] = round(us, 2)
+            row["algorithmic_tflops_under_counters"] = round(alg / us / 1e6, 1)
+        rows[name] = row
+    return {"m": m, "n": n, "k": k, "kernels": rows}
+
+
 if __name__ == "__main__":
+    if len(sys.argv) > 1 and sys.argv[1] == "tune":
+        sys.exit(tune_main(sys.argv[2:]))
+    if len(sys.argv) > 1 and sys.argv[1] == "prof":
+        sys.exit(prof_main(sys.argv[2:]))
     sys.exit(main())

@@ -4,6 +4,7 @@ that return before any launch, the tile layout, the W4Linear contract and dispat
 
 from __future__ import annotations
 
+import csv
 import ctypes
 import os
 import re
@@ -349,3 +350,53 @@ def test_bench_sweep_covers_the_single_linear_configs():
     assert got == want
     # the per-call byte count of the benchmark's metric: int4 weights, fp16 scales, int4 zeros, x and y
     assert bench.call_bytes(1, 4096, 24576) == 52355072
+
+
+def _bench_module():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    return bench
+
+
+def test_prof_summary_targets_the_profiled_kernel(tmp_path):
+    """bench.py prof --summarize headlines the kernel the command launched --launches times, never the
+    load-time repack that ran once per weight copy (more often than the kernel at M = 32), and scales
+    each counter by the calibration copy's reading."""
+    bench = _bench_module()
+    assert bench.target_kernel({"tw4::repack_weights_kernel": 80, "tw4::gemm_kernel<2,1>": 40,
+                                "other": 40}, 40) == "tw4::gemm_kernel<2,1>"
+    assert bench.target_kernel({"tw4::repack_weights_kernel": 80, "tw4::mma_kernel": 20}, 40) == "tw4::mma_kernel"
+    rows = []
+    for counter, copy_val, kern_val in (("FETCH_SIZE", 131072.0, 25000.0), ("WRITE_SIZE", 262144.0, 48.0)):
+        path = tmp_path / f"{counter}.csv"
+        with open(path, "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+            w.writeheader()
+            d = 0
+            for _ in range(3):
+                d += 1
+                w.writerow({"Dispatch_Id": d, "Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": counter,
+                            "Counter_Value": copy_val})
+            for _ in range(90):  # 90 repacks of the weight copies, then the 40 profiled launches
+                d += 1
+                w.writerow({"Dispatch_Id": d, "Kernel_Name": "tw4::repack_weights_kernel", "Counter_Name": counter,
+                            "Counter_Value": 999.0})
+            for _ in range(40):
+                d += 1
+                w.writerow({"Dispatch_Id": d, "Kernel_Name": "tw4::gemm_kernel", "Counter_Name": counter,
+                            "Counter_Value": kern_val})
+        rows.append(str(path))
+    rec = bench.summarize_traffic(rows[0], rows[1], 256, 3, 40, 52355072)
+    assert rec["kernel"] == "tw4::gemm_kernel" and rec["fetch_factor"] == 2.0 and rec["write_factor"] == 1.0
+    assert rec["hbm_bytes_per_launch"] == round((25000.0 * 2 + 48.0) * 1024)
+
+
+def test_bench_subcommands_parse():
+    """`bench.py tune` and `bench.py prof` take their own options (help exits 0 without a GPU)."""
+    for sub in ("tune", "prof"):
+        proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), sub, "--help"], capture_output=True,
+                              text=True, timeout=300)
+        assert proc.returncode == 0 and f"bench.py {sub}" in proc.stdout, proc.stderr

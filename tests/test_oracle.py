@@ -320,3 +320,31 @@ def test_planted_norm_mistakes_are_caught():
     assert not (y_bad == _norm_constant_row_expected(-1.5, 0.75, 1e-6)).all()  # the true s = -1.5
     y, _ = o.add_rms_norm(x, r, w, 1e-6)
     assert (y == _norm_constant_row_expected(-1.5, 0.75, 1e-6)).all()
+
+
+# ------------------------------------- the torch restatement of the fallback (CPU baseline)
+def test_torch_fallback_matches_numpy_oracle():
+    """oracle/torch_fallback.py (the CPU baseline's arithmetic) against the numpy oracle: the same
+    unpacked nibbles, the same dequantized fp16 bits (every element), and products inside the
+    fp16 GEMM tolerance of the float64 product; a copy with the pack order for the reverse order
+    fails the bit check."""
+    import torch
+
+    from oracle import torch_fallback as tf
+
+    data = np.load(os.path.join(GOLDEN, "awq_small.npz"))
+    qw, qz, s = (torch.from_numpy(data[n]) for n in ("qweight", "qzeros", "scales"))
+    assert (tf.unpack_awq(qw).numpy() == o.unpack_awq(data["qweight"])).all()
+    w = tf.dequant_kn(qw, qz, s)
+    assert (w.t().contiguous().numpy().view(np.uint16) == data["w_fp16"].view(np.uint16)).all()
+    x = torch.from_numpy(data["x"])
+    for dt in (torch.float16, torch.float32):
+        y = tf.fallback_linear(x, qw, qz, s, dt).double().numpy()
+        assert np.allclose(y, data["y_f64"], atol=0.05, rtol=0.02), dt
+    saved = tf._SHIFTS
+    try:
+        tf._SHIFTS = torch.tensor([4 * i for i in o.AWQ_PACK_ORDER], dtype=torch.int32)
+        bad = tf.dequant_kn(qw, qz, s).t().contiguous().numpy()
+        assert not (bad.view(np.uint16) == data["w_fp16"].view(np.uint16)).all()
+    finally:
+        tf._SHIFTS = saved
