@@ -4,6 +4,7 @@
     python bench.py --sweep [--sweep-out FILE]
     python bench.py tune [--model qwen3-8b] [--ms 1,4,8,16] [--kinds gemv,mma] ...
     python bench.py prof [--proj gate_up] [--m 1] [--launches 40] ...  |  prof --summarize ...
+    python bench.py floor
 
 One step = one decode token's W4A16 linears of the whole Qwen3-8B stack: 36 layers x {qkv
 (K 4096, N 6144), o (4096, 4096), gate_up (4096, 24576), down (12288, 4096)} at M = 1, launched
@@ -18,6 +19,7 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
                 on its own stream, against MI355X's 8 TB/s HBM peak; beside it the kernel-only
                 time of the committed rocprofv3 summary (profiles/roofline_gate_up_m1.json) and the
                 fraction that gives; `traffic` from that summary's FETCH_SIZE / WRITE_SIZE counters
+                and the plain-read floor at the same byte count (tw4_read_probe, see read_floor)
   cpu_baseline  the reference's fallback (dequantize the whole weight every call, then one matmul;
                 oracle/torch_fallback.py) in torch on this host's cores, on Qwen3-0.6B's qkv at M = 1
                 (the reference's CPU-runnable config) and on one Qwen3-8B layer at the benchmark's M:
@@ -41,7 +43,8 @@ M = 16 the dequantize + torch.matmul comparator. Each shape rotates over enough 
 
 `tune` times every compiled configuration of the chosen kernels per (shape, M) and prints the
 fastest (how layers/w4_tables.py was measured). `prof` is a fixed eager launch sequence for
-hardware-counter runs under rocprofv3, and summarizes their CSV files (see prof_main).
+hardware-counter runs under rocprofv3, and summarizes their CSV files (see prof_main). `floor` times
+the plain-read ceiling (tw4_read_probe) at each projection's byte count (see read_floor).
 """
 
 from __future__ import annotations
@@ -172,6 +175,49 @@ def sweep(torch, awq, dev, stream, out_path: str) -> int:
     return 0
 
 
+# ------------------------------------------------------------------------- plain-read floor
+FLOOR_WORKGROUPS = (256, 512, 1024, 2048, 4096)
+
+
+def read_floor(torch, dev, stream, nbytes: int) -> dict:
+    """The plain-read ceiling at one launch size: tw4_read_probe reading `nbytes` per launch, launches
+    back to back from one HIP graph over distinct slices of a >= 1 GB buffer (the decode kernels' own
+    regime), at the best of FLOOR_WORKGROUPS; us per launch and GB/s."""
+    from tandem_amd.layers import w4_hip
+
+    per = -(-nbytes // 256) * 256
+    copies = max(2, -(-(1 << 30) // per))
+    buf = torch.empty(copies * per // 2, dtype=torch.float16, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    slices = [buf[i * per // 2:i * per // 2 + nbytes // 2] for i in range(copies)]
+    best = None
+    for wg in FLOOR_WORKGROUPS:
+        g = graph_of(torch, lambda: [w4_hip.read_probe(v, sink, wg) for v in slices], stream)
+        us = time_graph(torch, g, stream, reps=max(3, 200 // copies)) / copies * 1e6
+        del g
+        if best is None or us < best[0]:
+            best = (us, wg)
+    del buf, slices
+    return {"bytes": nbytes, "us": round(best[0], 3), "GBps": round(nbytes / best[0] / 1e3, 1),
+            "pct_hbm_peak": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS * 100, 1), "workgroups": best[1],
+            "launches_per_graph": copies}
+
+
+def floor_main(argv=None) -> int:
+    """The plain-read floor at every Qwen3-8B projection's M = 1 byte count and at 1 GB (see read_floor);
+    one JSON line per size."""
+    import torch
+
+    ap = argparse.ArgumentParser(prog="bench.py floor", description=floor_main.__doc__.split("\n")[0])
+    ap.parse_args(argv)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    for name, nbytes in [(p, call_bytes(1, k, n)) for p, k, n in QWEN3_8B] + [("1GiB", 1 << 30)]:
+        print(json.dumps({"what": name, **read_floor(torch, dev, stream, nbytes)}), flush=True)
+    return 0
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def _cpu_model() -> str:
     try:
@@ -230,11 +276,14 @@ def cpu_baseline(m: int) -> dict:
         sec = median_s(lambda: [x @ w for x, w in pre])
         rec["matmul_only_predequantized_fp16"] = {"ms": round(sec * 1e3, 3), "GBps": round(b / sec / 1e9, 3)}
         res[label] = rec
-    main = res[f"qwen3_8b_layer_m{m}"]["fp16"]
+    layer = res[f"qwen3_8b_layer_m{m}"]
+    best = min(("fp16", "fp32"), key=lambda v: layer[v]["ms"])
+    main = layer[best]
     return {"value": main["GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"the reference's fallback (AWQ unpack + fp16 dequant of the whole weight every call, then "
                       f"one matmul) in torch on {threads} threads: one Qwen3-8B layer's qkv, o, gate_up and down at "
-                      f"M={m} (value: fp16 product) and Qwen3-0.6B qkv at M=1; 3 warm-ups + median of 10 calls "
+                      f"M={m} (value: the faster product, {best}) and Qwen3-0.6B qkv at M=1; 3 warm-ups + median "
+                      f"of 10 calls "
                       f"each; host {_cpu_model()} ({cores} cores visible); "
                       f"{time.perf_counter() - t_start:.1f} s in all",
             "ms_per_call": main["ms"], "variants": res}
@@ -369,6 +418,8 @@ def main(argv=None) -> int:
         roofline["profile_frac"] = round(gate_bytes / prof["kernel_us"] / 1e3 / HBM_PEAK_GBS, 4)
         roofline["profile"] = os.path.relpath(ROOFLINE_PROFILE, ROOT)
     del gate_graph
+    floor = read_floor(torch, dev, stream, gate_bytes)
+    roofline["read_floor"] = {**floor, "kernel_over_floor": round(gate_s * 1e6 / floor["us"], 3)}
 
     detail = {}
     if not a.no_detail:
@@ -795,4 +846,6 @@ if __name__ == "__main__":
         sys.exit(tune_main(sys.argv[2:]))
     if len(sys.argv) > 1 and sys.argv[1] == "prof":
         sys.exit(prof_main(sys.argv[2:]))
+    if len(sys.argv) > 1 and sys.argv[1] == "floor":
+        sys.exit(floor_main(sys.argv[2:]))
     sys.exit(main())

@@ -396,7 +396,7 @@ def test_prof_summary_targets_the_profiled_kernel(tmp_path):
 
 def test_bench_subcommands_parse():
     """`bench.py tune` and `bench.py prof` take their own options (help exits 0 without a GPU)."""
-    for sub in ("tune", "prof"):
+    for sub in ("tune", "prof", "floor"):
         proc = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), sub, "--help"], capture_output=True,
                               text=True, timeout=300)
         assert proc.returncode == 0 and f"bench.py {sub}" in proc.stdout, proc.stderr
