@@ -178,6 +178,24 @@ int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
              void* stream);
 
+/* tw4_gemm without a caller workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference: its w4_gemm always takes the Python-owned workspace (python/tandem/layers/w4_cuda.py:24-41).
+ * Same kernels, arguments (minus ws / locks / sizes), results and errors as tw4_gemm; the split-K
+ * partial sums and tile counters live in a static device array of the library, one per GPU, of
+ * TW4_NOALLOC_FLOATS fp32 values and TW4_NOALLOC_COUNTERS int32 counters, held until the process ends.
+ * A call whose split-K needs more is refused with TW4_ESPACE (splits = 0 only splits within the
+ * limit). The function allocates nothing and never synchronizes. tw4_init(device) sets the array up
+ * (its address and cleared counters); without it the first call on a device does, and then must not
+ * be under graph capture (TW4_EINVAL). All calls on one GPU share the array: calls that overlap on a
+ * GPU (other streams or threads) race and must be serialized by the caller. */
+#define TW4_NOALLOC_FLOATS (1LL << 21)
+#define TW4_NOALLOC_COUNTERS 16384
+int tw4_gemm_noalloc(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
+                     const uint16_t* zeros, uint16_t* y, int M, int N, int K,
+                     int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
+                     void* stream);
+
 /* Dense fp16 GEMV for small batches: y [M, N] = x [M, K] @ w [N, K]^T (w row-major, nn.Linear
  * layout), 1 <= M <= 8, K in {512, 1024, 2048, 4096}, fp32 accumulation; x and w 16-byte aligned.
  * Config: rows_inflight rows per wavefront in flight (plus the next block prefetched), rows_per_wave

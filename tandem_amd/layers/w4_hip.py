@@ -49,6 +49,7 @@ _SIGNATURES = {
     "tw4_mma_splitk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma_persist": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "tw4_gemm_noalloc": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
     "tw4_read_probe": ([_P, _I64, _I, ctypes.c_uint32, _P, _P], _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
@@ -274,6 +275,32 @@ class W4Extension:
                                     ws.numel(), locks.numel(), m, n, k, int(mt), int(nt), int(warps_n),
                                     int(warps_k), int(stages), int(splits), int(act), _stream(x)))
         return y
+
+    def w4_gemm_noalloc(self, x, w, s, z, mt: int, nt: int, warps_n: int, warps_k: int, stages: int, splits: int,
+                        act: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """w4_gemm with the library's static split-K scratch instead of a workspace (tw4_gemm_noalloc: the
+        C entry point allocates nothing). y comes from ``out`` (float16 [M, N] or [M, N / 2], contiguous,
+        on x's GPU) or is allocated here with torch. Calls on one GPU share the scratch and must not
+        overlap."""
+        m, n, k = check_operands("w4_gemm_noalloc", x, w, s, z)
+        if act not in (0, 1) or (act and n % 16):
+            raise RuntimeError("w4_gemm_noalloc: act 0, or 1 (SwiGLU) with N % 16 == 0")
+        if m * k >= 1 << 31:
+            raise RuntimeError("w4_gemm_noalloc: M x K < 2^31")
+        shape = (m, n // 2 if act else n)
+        if out is None:
+            out = torch.empty(shape, dtype=torch.float16, device=x.device)
+        elif (tuple(out.shape) != shape or out.dtype != torch.float16 or out.device != x.device
+              or not out.is_contiguous() or out.data_ptr() % 8):
+            raise RuntimeError(f"w4_gemm_noalloc: out must be a contiguous float16 {list(shape)} tensor on x's GPU")
+        if m == 0:
+            return out
+        with torch.cuda.device(x.device):
+            init_device(x.device)
+            check(self.lib.tw4_gemm_noalloc(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(out), m, n, k, int(mt), int(nt),
+                                            int(warps_n), int(warps_k), int(stages), int(splits), int(act),
+                                            _stream(x)))
+        return out
 
     def last_gemm_grid(self) -> tuple[int, int, int]:
         b, d, s = _I(), _I(), _I()
