@@ -178,12 +178,13 @@ def sweep(torch, awq, dev, stream, out_path: str) -> int:
 # ------------------------------------------------------------------------- plain-read floor
 FLOOR_WORKGROUPS = (256, 512, 1024, 2048, 4096)
 FLOOR_ORDERS = (False, True)  # grid-stride, chunked
+FLOOR_DEPTHS = (1, 2, 8)      # loads issued per lane before any is used
 
 
 def read_floor(torch, dev, stream, nbytes: int) -> dict:
     """The plain-read ceiling at one launch size: tw4_read_probe reading `nbytes` per launch, launches
     back to back from one HIP graph over distinct slices of a >= 1 GB buffer (the decode kernels' own
-    regime), at the best of FLOOR_WORKGROUPS x FLOOR_ORDERS; us per launch and GB/s."""
+    regime), at the best of FLOOR_DEPTHS x FLOOR_ORDERS x FLOOR_WORKGROUPS; us per launch and GB/s."""
     from tandem_amd.layers import w4_hip
 
     per = -(-nbytes // 256) * 256
@@ -192,17 +193,18 @@ def read_floor(torch, dev, stream, nbytes: int) -> dict:
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     slices = [buf[i * per // 2:i * per // 2 + nbytes // 2] for i in range(copies)]
     best = None
-    for chunked in FLOOR_ORDERS:
-        for wg in FLOOR_WORKGROUPS:
-            g = graph_of(torch, lambda: [w4_hip.read_probe(v, sink, wg, chunked) for v in slices], stream)
-            us = time_graph(torch, g, stream, reps=max(3, 200 // copies)) / copies * 1e6
-            del g
-            if best is None or us < best[0]:
-                best = (us, wg, chunked)
+    for depth in FLOOR_DEPTHS:
+        for chunked in FLOOR_ORDERS:
+            for wg in FLOOR_WORKGROUPS:
+                g = graph_of(torch, lambda: [w4_hip.read_probe(v, sink, wg, chunked, depth) for v in slices], stream)
+                us = time_graph(torch, g, stream, reps=max(3, 200 // copies)) / copies * 1e6
+                del g
+                if best is None or us < best[0]:
+                    best = (us, wg, chunked, depth)
     del buf, slices
     return {"bytes": nbytes, "us": round(best[0], 3), "GBps": round(nbytes / best[0] / 1e3, 1),
             "pct_hbm_peak": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS * 100, 1), "workgroups": best[1],
-            "order": "chunked" if best[2] else "grid-stride", "launches_per_graph": copies}
+            "order": "chunked" if best[2] else "grid-stride", "inflight": best[3], "launches_per_graph": copies}
 
 
 def floor_main(argv=None) -> int:
@@ -228,11 +230,12 @@ def floor_main(argv=None) -> int:
 
 def summarize_floor_trace(path: str) -> list[dict]:
     """The read-probe dispatches of a `bench.py floor` kernel trace, in launch order, cut into one run
-    per (size, order, workgroup count) as floor_main issues them (sizes in QWEN3_8B order then 1 GiB, each
-    over FLOOR_ORDERS x FLOOR_WORKGROUPS): per run the average and minimum kernel-only time and GB/s."""
+    per (size, depth, order, workgroup count) as floor_main issues them (sizes in QWEN3_8B order then 1 GiB,
+    each over FLOOR_DEPTHS x FLOOR_ORDERS x FLOOR_WORKGROUPS): per run the average and minimum kernel-only
+    time and GB/s."""
     with open(path, newline="", encoding="utf-8") as f:
         rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), int(r["Grid_Size_X"]),
-                       "chunked" in r["Kernel_Name"]) for r in csv.DictReader(f) if "read_probe" in r["Kernel_Name"])
+                       r["Kernel_Name"]) for r in csv.DictReader(f) if "read_probe" in r["Kernel_Name"])
     runs: list[list[tuple[int, int, int]]] = []
     for r in rows:
         if not runs or runs[-1][-1][2] != r[2] or runs[-1][-1][3] != r[3]:
@@ -240,13 +243,15 @@ def summarize_floor_trace(path: str) -> list[dict]:
         runs[-1].append(r)
     sizes = [(p, call_bytes(1, k, n)) for p, k, n in QWEN3_8B] + [("1GiB", 1 << 30)]
     out = []
-    per_size = len(FLOOR_WORKGROUPS) * len(FLOOR_ORDERS)
+    per_size = len(FLOOR_WORKGROUPS) * len(FLOOR_ORDERS) * len(FLOOR_DEPTHS)
     for i, run in enumerate(runs):
         what, nbytes = sizes[i // per_size] if i // per_size < len(sizes) else ("?", 0)
+        depth = FLOOR_DEPTHS[(i % per_size) // (len(FLOOR_WORKGROUPS) * len(FLOOR_ORDERS))]
         ns = [e - s for s, e, _, _ in run]
         avg, best = sum(ns) / len(ns), min(ns)
         out.append({"what": what, "bytes": nbytes, "workgroups": run[0][2] // 256,
-                    "order": "chunked" if run[0][3] else "grid-stride", "dispatches": len(ns),
+                    "order": "chunked" if "chunked" in run[0][3] else "grid-stride", "inflight": depth,
+                    "dispatches": len(ns),
                     "avg_us": round(avg / 1e3, 3), "min_us": round(best / 1e3, 3),
                     "avg_GBps": round(nbytes / avg, 1) if nbytes else None})
     return out

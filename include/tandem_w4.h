@@ -226,14 +226,15 @@ int tw4_add_rms_norm(uint16_t* x, uint16_t* residual, const uint16_t* weight, in
                      float eps, void* stream);
 
 /* Streaming-read probe: reads `bytes` (a multiple of 16) from the device buffer `src` with 16-byte
- * non-temporal loads (1 KB per wavefront instruction, 8 in flight per lane) over `workgroups`
+ * non-temporal loads (1 KB per wavefront instruction, `inflight` = 1, 2, 4 or 8 issued per lane
+ * before any is used) over `workgroups`
  * workgroups of 256 threads, grid-stride (chunked = 0) or one contiguous span per workgroup (chunked =
  * 1, the decode kernels' order), and does nothing else: it writes sink[0] only if the XOR of every
  * loaded word equals `key`. The plain-read ceiling against which the decode kernels' bandwidth is
  * judged. No reference counterpart (the reference calibrated with a device copy,
  * docs/P0基线报告.md:33). */
-int tw4_read_probe(const void* src, int64_t bytes, int workgroups, int chunked, uint32_t key, uint32_t* sink,
-                   void* stream);
+int tw4_read_probe(const void* src, int64_t bytes, int workgroups, int chunked, int inflight, uint32_t key,
+                   uint32_t* sink, void* stream);
 
 /* Compiled configurations, for sweeps and tests (the reference lists them in its host code,
  * python/tandem/csrc/w4_gemv.cu:596-597, 641-645, 676-679). Each writes up to max_configs

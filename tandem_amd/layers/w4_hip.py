@@ -51,7 +51,7 @@ _SIGNATURES = {
     "tw4_gemm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_noalloc": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
-    "tw4_read_probe": ([_P, _I64, _I, _I, ctypes.c_uint32, _P, _P], _I),
+    "tw4_read_probe": ([_P, _I64, _I, _I, _I, ctypes.c_uint32, _P, _P], _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemv_f16": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
@@ -351,10 +351,10 @@ def dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, dei
 
 
 def read_probe(buf: torch.Tensor, sink: torch.Tensor, workgroups: int = 2048, chunked: bool = False,
-               key: int = 0x9E3779B9) -> None:
+               inflight: int = 1, key: int = 0x9E3779B9) -> None:
     """Read every byte of the contiguous GPU tensor ``buf`` once with 16-byte streaming loads and nothing
-    else (tw4_read_probe), grid-stride or one contiguous span per workgroup (``chunked``), on the current
-    stream: the plain-read ceiling of HBM. ``sink``: an int32 GPU tensor written only if the XOR of the
+    else (tw4_read_probe), grid-stride or one contiguous span per workgroup (``chunked``), ``inflight``
+    loads issued per lane before any is used, on the current stream: the plain-read ceiling of HBM. ``sink``: an int32 GPU tensor written only if the XOR of the
     data equals ``key``."""
     if not (buf.is_cuda and buf.is_contiguous() and buf.data_ptr() % 16 == 0 and (buf.numel() * buf.element_size()) % 16 == 0):
         raise RuntimeError("read_probe: a contiguous 16-byte aligned GPU tensor of a multiple of 16 bytes")
@@ -362,7 +362,7 @@ def read_probe(buf: torch.Tensor, sink: torch.Tensor, workgroups: int = 2048, ch
         raise RuntimeError("read_probe: sink must be an int32 tensor on the buffer's GPU")
     with torch.cuda.device(buf.device):
         check(library().tw4_read_probe(_ptr(buf), buf.numel() * buf.element_size(), int(workgroups), int(bool(chunked)),
-                                       key & 0xFFFFFFFF, _ptr(sink), _stream(buf)))
+                                       int(inflight), key & 0xFFFFFFFF, _ptr(sink), _stream(buf)))
 
 
 def workspace(device: torch.device | str | int) -> tuple[torch.Tensor, torch.Tensor]:
