@@ -165,6 +165,10 @@ int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* sc
  *           each wavefront streams its weight blocks with two groups in flight (every tile is
  *           split: splits = 0 picks the fewest splits whose x slice fits, then enough units to
  *           fill the GPU; a slice that cannot fit is refused with TW4_ECONFIG)
+ *           3: large M: x AND the int4 weight tiles staged through LDS by direct-to-LDS loads
+ *           (global_load_lds_dwordx4) in a 3-deep ring of half-group (64 k) stages; warps_k is then
+ *           the number of wavefronts along M (BM = 16 mt warps_k, BN = 16 nt warps_n); N % 16 == 0,
+ *           scales and zeros 16-byte aligned; splits = 0 picks enough K splits to fill the GPU
  *   splits  0: split only the last, partial wave of tiles along K; 1: no split; s > 1: every
  *           tile split s ways
  * ws (fp32, ws_floats) and locks (int32, n_locks, zero before the first call) are the split-K
@@ -239,7 +243,8 @@ int tw4_read_probe(const void* src, int64_t bytes, int workgroups, int chunked, 
 /* Compiled configurations, for sweeps and tests (the reference lists them in its host code,
  * python/tandem/csrc/w4_gemv.cu:596-597, 641-645, 676-679). Each writes up to max_configs
  * tuples into out and returns how many exist: tw4_decode_configs (warps_k, unroll, ntile) for
- * tw4_gemv and tw4_mma; tw4_gemm_configs (mt, nt, warps_n, warps_k, stages) for tw4_gemm. */
+ * tw4_gemv and tw4_mma; tw4_gemm_configs (mt, nt, warps_n, warps_k, stages) for tw4_gemm (for
+ * stages 3 the fourth value is the wavefronts along M). */
 int tw4_decode_configs(int* out, int max_configs);
 int tw4_gemm_configs(int* out, int max_configs);
 

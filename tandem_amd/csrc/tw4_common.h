@@ -210,6 +210,15 @@ __host__ __device__ __forceinline__ int interleaved_dest_row(int src, int n) {
     return 16 * (rem >> 3) + 8 * h + (rem & 7);
 }
 
+// Workgroups are dealt to the 8 XCDs round robin (workgroup b runs on XCD b mod 8); renumbering them so
+// that XCD x gets a contiguous range of work units keeps the units that share weight or x tiles in one
+// XCD's L2. A permutation of 0 .. n - 1 (the first n mod 8 XCDs take one unit more).
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+    if (n < 16) return b;
+    const int q = n >> 3, rr = n & 7, xcd = b & 7, idx = b >> 3;
+    return xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
+}
+
 // The end of a work unit, run by every thread of the workgroup. Wavefronts with `holder` set hold
 // the unit's fp32 tiles (rows 16 (wt0 + t) .., tokens m0 + 16 b ..) in acc. nsplit > 1: each stores
 // its partial to split slot su of ws; one agent-scope counter per split tile (st) tells the last

@@ -47,11 +47,6 @@ struct GemmCfg {
     static constexpr int LDS = RING > RED ? RING : RED;
 };
 
-__device__ __forceinline__ int xcd_remap(int b, int n) {
-    if (n < 16) return b;
-    const int q = n >> 3, rr = n & 7, xcd = b & 7, idx = b >> 3;
-    return xcd < rr ? xcd * (q + 1) + idx : rr * (q + 1) + (xcd - rr) * q + idx;
-}
 
 template <int MT, int NT, int WN, int WK, int ST>
 __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
@@ -579,6 +574,12 @@ using namespace tw4;
 
 int tw4_gemm_prepare_device(int dev) { return device_prepare(dev); }
 
+// tw4_gemm_lds.hip: the stages-3 GEMM (weights and x staged in LDS by direct-to-LDS loads)
+int tw4_gemm_lds_dispatch(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                          uint16_t* y, float* ws, int32_t* locks, int64_t ws_floats, int64_t n_locks, int M, int N,
+                          int K, int mt, int nt, int warps_n, int warps_m, int splits, int cus, int act, void* stream);
+int tw4_gemm_lds_configs(int* out, int max_configs, int start);
+
 extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
                         uint16_t* y, float* ws, int32_t* locks, int64_t ws_floats, int64_t n_locks, int M, int N,
                         int K, int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,
@@ -603,6 +604,9 @@ extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t
         if (rc) return rc;
     }
     if (splits == 0 && !(ws && locks)) splits = 1;
+    if (stages == 3)
+        return tw4_gemm_lds_dispatch(x, packed, scales, zeros, y, ws, locks, ws_floats, n_locks, M, N, K, mt, nt,
+                                     warps_n, warps_k, splits, g_dev[dev].cus, act, stream);
     auto xp = reinterpret_cast<const h1*>(x);
     auto wp = reinterpret_cast<const u4*>(packed);
     auto sp = reinterpret_cast<const h1*>(scales);
@@ -663,5 +667,5 @@ extern "C" int tw4_gemm_configs(int* out, int max_configs) {
     TW4_STREAM_CONFIGS(TW4_SLIST)
 #undef TW4_LIST
 #undef TW4_SLIST
-    return n;
+    return n + tw4_gemm_lds_configs(out, max_configs, n);
 }

@@ -173,9 +173,10 @@ W4_KERNELS: dict[str, dict[tuple, W4Kernel]] = {
 # LDS ring, SPLITS: split-K of every tile, or 0: of the last, partial wave of tiles only), or
 # ("mma", warps_k, unroll, ntile): the streaming matrix-core kernel of the decode path, whose 16-token
 # batch tiles cover M <= 64 (bandwidth-bound batches), or None: dequantize to float16 +
-# torch.matmul. Shapes without an entry use DEFAULT_GEMM, which ends like every measured gfx950
-# ladder: past M = 1024 the dequantize + hipBLASLt pair beats the fused GEMM (by ~30% at M = 4096 on
-# the Qwen3-8B shapes), since the one-off dequant is small next to the product there.
+# torch.matmul. Shapes without an entry use DEFAULT_GEMM, which stops at M = 1024 like the measured
+# gfx950 ladders before the GEMM with both tiles staged through LDS (stages 3): on the Qwen3-8B shapes
+# that GEMM carries the fused path to M = 2048, and past it the dequantize + hipBLASLt pair wins (by
+# ~20 % at M = 4096), since the one-off dequant is small next to the product there.
 # TANDEM_W4_GEMM=0: always dequantize + torch.matmul (python/tandem/layers/awq.py:163-186).
 W4Gemm = tuple
 DEFAULT_GEMM: tuple[tuple[int, W4Gemm | None], ...] = (

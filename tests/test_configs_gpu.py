@@ -108,10 +108,10 @@ def test_qwen3_8b_prefill_sizes(proj, silu):
         xg = gpu(x)
         ref = sampled_reference(x, t, feats, n, silu)
         runs = [("table", awq.pick_gemm(table, m), layer(xg))]
-        if m == 4096:
-            cfg = (8, 2, 4, 1, 2, 1)  # 128 x 128 tiles, LDS ring, no split: the fused path at prefill size
-            runs.append(("forced gemm", cfg, ext.w4_gemm(xg, layer.packed, layer.scales, layer.zeros, buf, locks, *cfg,
-                                                         int(silu))))
+        if m == 4096:  # the fused path at prefill size: x through the LDS ring, and both tiles through LDS
+            for cfg in ((8, 2, 4, 1, 2, 1), (8, 4, 4, 2, 3, 1), (16, 4, 4, 1, 3, 0)):
+                runs.append(("forced gemm", cfg, ext.w4_gemm(xg, layer.packed, layer.scales, layer.zeros, buf, locks,
+                                                             *cfg, int(silu))))
         for what, cfg, y in runs:
             assert y.shape == (m, n_out)
             got = y[:, torch.from_numpy(feats).to(DEV)].float().cpu().numpy()
