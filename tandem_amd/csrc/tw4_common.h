@@ -223,13 +223,19 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 // the unit's fp32 tiles (rows 16 (wt0 + t) .., tokens m0 + 16 b ..) in acc. nsplit > 1: each stores
 // its partial to split slot su of ws; one agent-scope counter per split tile (st) tells the last
 // arriver, which adds the nsplit partials of the tile in split order (the result does not depend
-// on arrival order), returns the counter to zero for the next call and writes y. Partials and their
-// reads are agent-scope relaxed atomics (global_store / global_load sc1: coherent across the
-// XCDs' L2s without a cache-wide write-back or invalidate); each wavefront partial is stored
-// [fragment][component][lane], so every instruction moves 256 contiguous bytes. s_waitcnt vmcnt(0)
-// + barrier order the stores before the count. act = 1: SwiGLU epilogue (gate rows 4 kb + i and
-// up rows 8 + 4 kb + i sit in lanes l and l + 32).
-template <int MT, int NT, int WN>
+// on arrival order), returns the counter to zero for the next call and writes y. Each wavefront
+// partial is stored [fragment][lane][component]: one 16-byte store or load per lane and fragment,
+// 1 KB contiguous per instruction. Stores and loads carry sc1, the cache policy of agent-scope
+// atomics on gfx950 (the compiler's relaxed agent-scope load / store): they are coherent across
+// the XCDs' L2s without a cache-wide write-back or invalidate. s_waitcnt vmcnt(0) + barrier order
+// the stores before the count; the last arriver issues its loads only after it has seen the count
+// reach nsplit. The last arriver loads the partials of VB splits at a time (one memory round trip
+// per VB splits) and adds them in split order. act = 1: SwiGLU epilogue (gate rows 4 kb + i and up
+// rows 8 + 4 kb + i sit in lanes l and l + 32).
+constexpr int kCoherentAux = 16;  // buffer-instruction cache policy: sc1
+constexpr int64_t kMaxPartialFloats = int64_t(1) << 29;  // split-K workspace used: byte offsets < 2^31
+
+template <int MT, int NT, int WN, int PART_FLOATS = 64>
 __device__ __forceinline__ void finish_unit(f4 (&acc)[NT][MT], bool holder, int wn, int lane, int tid, int nsplit,
                                             int st, int su, float* __restrict__ ws, int* __restrict__ locks,
                                             int& last_flag, h1* __restrict__ y, int M, int N, int m0, int wt0,
@@ -237,16 +243,16 @@ __device__ __forceinline__ void finish_unit(f4 (&acc)[NT][MT], bool holder, int 
     const int r = lane & 15, kb = lane >> 4;
     if (nsplit > 1) {
         constexpr int V = NT * MT * 4 * 64;  // floats per wavefront partial
+        // byte offsets below 2^31: the launchers use at most kMaxPartialFloats of the workspace
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ws, 0, 0x7FFFFFFF, kBufferFlags);
         if (holder) {
-            float* mine = ws + (static_cast<int64_t>(su) * WN + wn) * V + lane;
+            const int mine = static_cast<int>((static_cast<int64_t>(su) * WN + wn) * V * 4);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int b = 0; b < MT; ++b)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        __hip_atomic_store(mine + ((t * MT + b) * 4 + c) * 64, acc[t][b][c], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    __builtin_amdgcn_raw_buffer_store_b128(bitcast<u4>(acc[t][b]), rs, ((t * MT + b) * 64 + lane) * 16,
+                                                           mine, kCoherentAux);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -257,20 +263,31 @@ __device__ __forceinline__ void finish_unit(f4 (&acc)[NT][MT], bool holder, int 
         __syncthreads();
         if (!last_flag) return;
         if (holder) {
+            constexpr int F = NT * MT;                        // 16-byte fragments per lane of one partial
+            constexpr int VB = 4 * F >= PART_FLOATS ? 1 : PART_FLOATS / (4 * F);  // splits per round
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int b = 0; b < MT; ++b) acc[t][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            for (int v = 0; v < nsplit; ++v) {
-                const float* other = ws + ((static_cast<int64_t>(st) * nsplit + v) * WN + wn) * V + lane;
+            for (int v0 = 0; v0 < nsplit; v0 += VB) {
+                f4 part[VB][F];
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
+                for (int j = 0; j < VB; ++j) {
+                    const int v = min(v0 + j, nsplit - 1);  // past the last split: re-read it, not added
+                    const int other = static_cast<int>(((static_cast<int64_t>(st) * nsplit + v) * WN + wn) * V * 4);
 #pragma unroll
-                    for (int b = 0; b < MT; ++b)
+                    for (int i = 0; i < F; ++i)
+                        part[j][i] = bitcast<f4>(__builtin_amdgcn_raw_buffer_load_b128(rs, (i * 64 + lane) * 16, other,
+                                                                                       kCoherentAux));
+                }
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            acc[t][b][c] += __hip_atomic_load(other + ((t * MT + b) * 4 + c) * 64, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
+                for (int j = 0; j < VB; ++j) {
+                    if (v0 + j >= nsplit) break;  // uniform
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int b = 0; b < MT; ++b) acc[t][b] += part[j][t * MT + b];
+                }
             }
         }
         if (tid == 0) __hip_atomic_store(locks + st, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -1302,6 +1302,7 @@ extern "C" int tw4_mma_splitk(const uint16_t* x, const int32_t* packed, const ui
                 "mma: splits in 1 .. min(16, K / 128) (splits = %d, K = %d)", splits, K);
     TW4_REQUIRE(splits == 1 || M <= 16, TW4_EINVAL, "mma: split-K for M <= 16 only (M = %d)", M);
     TW4_REQUIRE(splits == 1 || (ws && locks), TW4_EINVAL, "mma: split-K needs a workspace and counters");
+    ws_floats = ws_floats < kMaxPartialFloats ? ws_floats : kMaxPartialFloats;  // the part split-K may use
     rc = ensure_prepared();
     if (rc) return rc;
     return mma_launch(reinterpret_cast<const h1*>(x), reinterpret_cast<const u4*>(packed),

@@ -56,7 +56,7 @@ __global__ void __launch_bounds__(WN * WK * 64) gemm_kernel(
     using C = GemmCfg<MT, NT, WN, WK, ST>;
     extern __shared__ u4 lds[];
     __shared__ int last_flag;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WN, wk = wave / WN;
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles_n = (N + 15) >> 4;
@@ -595,6 +595,8 @@ extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t
                 "gemm: act 0, or 1 (SwiGLU) with N %% 16 == 0 (act = %d, N = %d)", act, N);
     TW4_REQUIRE(splits >= 0 && splits <= 16, TW4_EINVAL, "gemm: splits 0 (split the last wave) or 1 .. 16");
     TW4_REQUIRE(splits <= 1 || (ws && locks), TW4_EINVAL, "gemm: split-K needs a workspace and counters");
+    TW4_REQUIRE(ws_floats >= 0 && n_locks >= 0, TW4_EINVAL, "gemm: workspace sizes must be >= 0");
+    ws_floats = ws_floats < kMaxPartialFloats ? ws_floats : kMaxPartialFloats;  // the part split-K may use
     if (M == 0) return TW4_OK;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
