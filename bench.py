@@ -271,8 +271,8 @@ def cpu_baseline(m: int) -> dict:
     whole weight every call, then one product; python/tandem/layers/awq.py:282-286) on this host:
     Qwen3-0.6B's qkv (K 1024, N 4096) at M = 1 and one Qwen3-8B layer's four projections at M, each
     with the product in fp16 and in fp32 and the pre-dequantized matmul alone; 3 warm-ups, then the
-    median of 10 timed calls. `value` is the 8B layer's fp16 variant in GB/s of the same
-    algorithmic bytes as the GPU figure."""
+    median of 10 timed calls. `value` is the 8B layer's faster variant (fp16 or fp32 product) in GB/s
+    of the same algorithmic bytes as the GPU figure."""
     import numpy as np
     import torch
 
