@@ -732,10 +732,16 @@ def prof_main(argv=None) -> int:
     ap.add_argument("--cfg", default="", help="GEMM config mt,nt,warps_n,warps_k,stages,splits for every M > 16")
     ap.add_argument("--summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--summarize-mfma", metavar="COUNTER_CSV")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
+                    help="per-dispatch medians of every counter of the profiled kernel, over one or more counter "
+                         "passes of the same command, with busy shares per XCD (see summarize_counters)")
     a = ap.parse_args(argv)
     k, n = PROF_SHAPES[a.proj]
     if a.summarize_mfma:
         print(json.dumps(summarize_mfma(a.summarize_mfma, a.m, n, k), indent=1))
+        return 0
+    if a.summarize_counters:
+        print(json.dumps(summarize_counters(a.summarize_counters, a.launches), indent=1))
         return 0
     if a.summarize:
         alg = call_bytes(a.m, k, n) - (a.m * n if a.silu else 0)
@@ -878,6 +884,66 @@ def summarize_mfma(path: str, m: int, n: int, k: int) -> dict:
             row["algorithmic_tflops_under_counters"] = round(alg / us / 1e6, 1)
         rows[name] = row
     return {"m": m, "n": n, "k": k, "kernels": rows}
+
+
+def summarize_counters(paths: list[str], launches: int) -> dict:
+    """The profiled kernel of `bench.py prof` counter runs (the tw4 kernel with exactly `launches`
+    dispatches, never a load-time repack): the median per dispatch of every counter in the given
+    counter_collection.csv files (one per --pmc pass) and of the kernel duration, plus derived shares.
+    The SQ counters and GRBM_GUI_ACTIVE are summed over the 8 XCDs, so GRBM_GUI_ACTIVE / 8 is the
+    kernel's clock cycles and a busy share is cycles / (cycles x 1024 SIMDs):
+      mfma_busy   SQ_VALU_MFMA_BUSY_CYCLES          (the matrix cores)
+      valu_busy   SQ_ACTIVE_INST_VALU x 4            (a wave64 VALU instruction holds a SIMD 4 cycles;
+                                                      SQ_INSTS_VALU counts the MFMA instructions too)
+      coexec      SQ_VALU_MFMA_COEXEC_CYCLES         (VALU and matrix cores busy in the same cycle)
+    and per dispatch the instructions per wavefront and the L2 hit share TCC_HIT / (TCC_HIT + TCC_MISS)."""
+    import statistics as st
+
+    vals: dict[str, list[float]] = {}
+    dur: list[float] = []
+    name = None
+    for path in paths:
+        rows: dict[str, list[dict]] = {}
+        with open(path, newline="", encoding="utf-8") as f:
+            for row in csv.DictReader(f):
+                rows.setdefault(row["Kernel_Name"], []).append(row)
+        cands = [k for k in rows if "tw4" in k and not any(t in k for t in LOAD_TIME_KERNELS)
+                 and len({r["Dispatch_Id"] for r in rows[k]}) == launches]
+        if len(cands) != 1:
+            raise SystemExit(f"{path}: {len(cands)} tw4 kernels with {launches} dispatches: {cands}")
+        name = cands[0]
+        seen = set()
+        for r in rows[name]:
+            vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            if r["Dispatch_Id"] not in seen and r.get("Start_Timestamp"):
+                seen.add(r["Dispatch_Id"])
+                dur.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    med = {c: st.median(v) for c, v in vals.items()}
+    out = {"kernel": name, "dispatches_timed": len(dur), "us_under_counters": round(st.median(dur), 2) if dur else None,
+           "counters": med}
+    cyc = med.get("GRBM_GUI_ACTIVE", 0) / 8
+    if cyc and dur and cyc / (st.median(dur) * 1e3) > 2.6:
+        # on a kernel of a few us GRBM_GUI_ACTIVE also counts around the dispatch (it implies a clock
+        # above the 2.4 GHz peak): take the duration at the peak clock instead (shares are then lower bounds)
+        out["cycles_basis"] = "duration x 2.4 GHz (GRBM_GUI_ACTIVE / 8 implied %.2f GHz)" % (cyc / (st.median(dur) * 1e3))
+        cyc = st.median(dur) * 1e3 * 2.4
+    elif cyc:
+        out["cycles_basis"] = "GRBM_GUI_ACTIVE / 8"
+    if cyc:
+        simd = 1024 * cyc
+        out["clock_GHz"] = round(cyc / (st.median(dur) * 1e3), 3) if dur else None
+        for key, cnt, mul in (("mfma_busy", "SQ_VALU_MFMA_BUSY_CYCLES", 1), ("valu_busy", "SQ_ACTIVE_INST_VALU", 4),
+                              ("coexec", "SQ_VALU_MFMA_COEXEC_CYCLES", 1), ("lds_busy", "SQ_ACTIVE_INST_LDS", 4)):
+            if cnt in med:
+                out[key] = round(med[cnt] * mul / simd, 4)
+    waves = med.get("SQ_WAVES")
+    if waves:
+        out["per_wavefront"] = {c: round(med[c] / waves, 1) for c in
+                                ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_INSTS_SALU")
+                                if c in med}
+    if "TCC_HIT_sum" in med and "TCC_MISS_sum" in med:
+        out["l2_hit_share"] = round(med["TCC_HIT_sum"] / max(med["TCC_HIT_sum"] + med["TCC_MISS_sum"], 1), 3)
+    return out
 
 
 if __name__ == "__main__":

@@ -165,6 +165,11 @@ int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* sc
  *           each wavefront streams its weight blocks with two groups in flight (every tile is
  *           split: splits = 0 picks the fewest splits whose x slice fits, then enough units to
  *           fill the GPU; a slice that cannot fit is refused with TW4_ECONFIG)
+ *           1: batched decode, M <= 16 mt (mt 1, 2 or 4): no x staging; each wavefront streams its
+ *           nt row tiles' weights and reads its x fragments from L2 (coalesced, then a cross-lane
+ *           transpose), both one quant group ahead of the math; warps_n is then the groups per
+ *           prefetch chunk (1 or 2) and warps_k the wavefronts splitting each unit's groups (4 or 8);
+ *           splits = 0 picks enough K splits to give every CU a unit
  *           3: large M: x AND the int4 weight tiles staged through LDS by direct-to-LDS loads
  *           (global_load_lds_dwordx4) in a 3-deep ring of half-group (64 k) stages; warps_k is then
  *           the number of wavefronts along M (BM = 16 mt warps_k, BN = 16 nt warps_n); N % 16 == 0,

@@ -32,6 +32,13 @@
 
 #include "tw4_common.h"
 
+// tw4_mid.hip: the stages-1 kernel (batched decode, 16 < M <= 64)
+int tw4_gemm_mid_prepare(int dev);
+int tw4_gemm_mid_dispatch(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,
+                          uint16_t* y, float* ws, int32_t* locks, int64_t ws_floats, int64_t n_locks, int M, int N,
+                          int K, int mt, int nt, int unroll, int warps_k, int splits, int cus, int act, void* stream);
+int tw4_gemm_mid_configs(int* out, int max_configs, int start);
+
 namespace tw4 {
 
 template <int MT, int NT, int WN, int WK, int ST>
@@ -564,6 +571,7 @@ int device_prepare(int dev) {
     if (rc == TW4_OK) rc = stream_prepare<MT, NT, WN, WK>();
     TW4_STREAM_CONFIGS(TW4_SPREP)
 #undef TW4_SPREP
+    if (rc == TW4_OK) rc = tw4_gemm_mid_prepare(dev);
     if (rc == TW4_OK) g_dev[dev].ready = 1;
     return rc;
 }
@@ -606,6 +614,9 @@ extern "C" int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t
         if (rc) return rc;
     }
     if (splits == 0 && !(ws && locks)) splits = 1;
+    if (stages == 1)
+        return tw4_gemm_mid_dispatch(x, packed, scales, zeros, y, ws, locks, ws_floats, n_locks, M, N, K, mt, nt,
+                                     warps_n, warps_k, splits, g_dev[dev].cus, act, stream);
     if (stages == 3)
         return tw4_gemm_lds_dispatch(x, packed, scales, zeros, y, ws, locks, ws_floats, n_locks, M, N, K, mt, nt,
                                      warps_n, warps_k, splits, g_dev[dev].cus, act, stream);
@@ -669,5 +680,6 @@ extern "C" int tw4_gemm_configs(int* out, int max_configs) {
     TW4_STREAM_CONFIGS(TW4_SLIST)
 #undef TW4_LIST
 #undef TW4_SLIST
-    return n + tw4_gemm_lds_configs(out, max_configs, n);
+    n += tw4_gemm_lds_configs(out, max_configs, n);
+    return n + tw4_gemm_mid_configs(out, max_configs, n);
 }

@@ -5,8 +5,11 @@
 // (wm, wn) computes 16 MT tokens x 16 NT rows. A stage is half a quant group (BK = 64 k): stage s
 // covers k = 64 s .. 64 s + 63 of group s / 2.
 //   x:       the BM x 64 fp16 tile, 128 B per token row, 8 rows per load instruction. LDS slot
-//            (row rho, position p) holds 16-byte chunk p ^ (rho & 7) of the row, so the 16 lanes of a
-//            B-fragment read (16 rows, one chunk) hit 8 different bank groups per 8 lanes.
+//            (row rho, position p) holds 16-byte chunk p ^ ((rho >> 1) & 7) of the row. Two rows fill
+//            the 64 banks, even rows the lower 32, odd rows the upper 32; the swizzle gives the 8
+//            even (and the 8 odd) rows of a B-fragment read (16 rows, one chunk) 8 different 16-byte
+//            positions, so its 16 lanes touch every bank once (with rho & 7, each position came
+//            twice: a 2-way bank conflict on every x read).
 //   weights: the int4 tile as it sits in HBM: the k half of each (row tile, group) 1 KB block is 512
 //            contiguous bytes (words kb = 2 h, 2 h + 1 of [kb][r][s]), two row tiles per instruction.
 //            Every weight byte is read from HBM once per workgroup; the WM wavefronts that share a
@@ -35,16 +38,19 @@ typedef __attribute__((address_space(3))) const void lds_void;
 // read; the ring waits with explicit vmcnt counts instead, and the loop holds no other vector memory
 // operation. M0 (the LDS base operand) is saved and restored around the load, one wait state after
 // writing it (the M0 -> LDS-DMA hazard).
+// The global address is a wavefront-uniform 64-bit base in SGPRs (`sbase`, the part that moves with the
+// stage) plus this lane's 32-bit byte offset `voff` (fixed for the whole kernel), the instruction's
+// scalar-base form: no per-lane 64-bit address arithmetic per load.
 template <int BYTES>
-__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds_addr) {
+__device__ __forceinline__ void lds_dma(const void* sbase, uint32_t voff, uint32_t lds_addr) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr);
     uint32_t saved;
     if constexpr (BYTES == 16)
-        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                     : "=&s"(saved) : "v"(src), "s"(base) : "memory");
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(base) : "memory");
     else
-        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                     : "=&s"(saved) : "v"(src), "s"(base) : "memory");
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(base) : "memory");
 }
 
 template <int MT, int NT, int WM, int WN>
@@ -55,15 +61,19 @@ struct LdsGemmCfg {
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int X_U4 = BM * 8;               // x tile: BM rows x 8 chunks
     static constexpr int W_U4 = BN / 16 * 32;         // weights: BN / 16 half-blocks of 512 B
-    static constexpr int P_U4 = WAVES * NT * 4;       // params: per wavefront NT x (16 scales, 16 zeros)
+    static constexpr int P_U4 = WAVES * 32;           // params: per wavefront 8 tiles' 16 scales, then their zeros
     static constexpr int SLOT_U4 = X_U4 + W_U4 + P_U4;
     static constexpr int X_INSTR = BM / 8 / WAVES;    // x loads per wavefront per stage (8 rows each)
     static constexpr int W_INSTR = BN / 32 / WAVES;   // weight loads per wavefront per stage (2 half-blocks)
-    static constexpr int P_INSTR = NT / 4;            // params loads per wavefront (4 tiles x 64 B each)
+    static constexpr int P_INSTR = 2;                 // params loads per wavefront: scales, zeros (8 tiles x 32 B)
     static constexpr int LOADS = X_INSTR + W_INSTR + P_INSTR;
+    // registers for two wavefronts per SIMD (at most 256 each) where the accumulators allow it and two
+    // wavefronts per SIMD can be resident: 8 wavefronts per workgroup, or 4 with a ring small enough
+    // (BM = 128) that two workgroups share a CU and run out of phase
+    static constexpr int MIN_WAVES_PER_SIMD = MT * NT <= 32 && (WAVES >= 8 || BM <= 128) ? 2 : 1;
     static_assert(BM % (8 * WAVES) == 0, "x rows split evenly over the wavefronts");
     static_assert(BN % (32 * WAVES) == 0, "weight half-blocks split evenly over the wavefronts");
-    static_assert(NT % 4 == 0, "params loads of 64 lanes x 4 bytes: 4 tiles x 64 B each");
+    static_assert(NT == 4 || NT == 8, "params: one dword load covers 8 tiles' 16 values (NT = 4 loads 4 twice)");
     static_assert(3 * LOADS < 64, "s_waitcnt vmcnt immediate");
 };
 
@@ -85,52 +95,61 @@ __device__ __forceinline__ void ring_barrier() {
 
 template <int MT, int NT, int WM, int WN>
 struct LdsGemmArgs {
-    const h1* x;
-    const u4* w;
-    const uint16_t* s16;
-    const uint16_t* z16;
-    int M, K, G, m0, tile0;  // tile0: the workgroup's first row tile
-    int tile_last;           // the matrix's last row tile: tiles past it read it again (never stored)
+    using C = LdsGemmCfg<MT, NT, WM, WN>;
+    const char* x;  // byte bases; a stage adds its k offset to them (scalar) and each lane its offset below
+    const char* w;
+    const char* s16;
+    const char* z16;
+    uint32_t xoff[C::X_INSTR];  // this lane's byte offsets, fixed for the kernel (see lds_gemm_offsets)
+    uint32_t woff[C::W_INSTR];
+    uint32_t poff;              // scales and zeros share it
 };
 
-// Issue the direct-to-LDS loads of stage `st` into `slot`. Every wavefront issues exactly LOADS
-// instructions, so each can wait for a stage with one vmcnt.
+// Per-lane byte offsets of the direct-to-LDS loads (everything but the stage's k position):
+//   x load i (rows 8 j .. 8 j + 7 of the tile, j = wave X_INSTR + i): lane l takes row rho = 8 j + l / 8
+//     (rows past M read the last row; never stored), 16-byte chunk (l & 7) ^ ((rho >> 1) & 7);
+//   weight load i (row tiles 2 j, 2 j + 1 of the workgroup, j = wave W_INSTR + i): lane l the 16 bytes
+//     l & 31 of the k half of tile 2 j + l / 32's block (tiles past the matrix read its last tile);
+//   params: lane l the values of rows 2 (l & 7), + 1 of the wavefront's tile l / 8 (of NT; NT = 4 repeats).
 template <int MT, int NT, int WM, int WN>
-__device__ __forceinline__ void issue_stage(uint32_t slot, const LdsGemmArgs<MT, NT, WM, WN>& a, int st, int wave,
-                                            int lane) {
+__device__ __forceinline__ void lds_gemm_offsets(LdsGemmArgs<MT, NT, WM, WN>& a, int M, int K, int G, int m0,
+                                                 int tile0, int tile_last, int wave, int wn, int lane) {
     using C = LdsGemmCfg<MT, NT, WM, WN>;
-    const int g = st >> 1, h = st & 1;
-    // x: rows 8 j .. 8 j + 7 of the tile for instruction j = wave X_INSTR + i
 #pragma unroll
     for (int i = 0; i < C::X_INSTR; ++i) {
         const int j = wave * C::X_INSTR + i;
-        const int rho = 8 * j + (lane >> 3), p = lane & 7, c = p ^ (rho & 7);
-        const int row = min(a.m0 + rho, a.M - 1);  // rows past M repeat the last one; never stored
-        const h1* src = a.x + static_cast<int64_t>(row) * a.K + 128 * g + 64 * h + 8 * c;
-        lds_dma<16>(src, slot + 16 * 64 * j);
+        const int rho = 8 * j + (lane >> 3), c = (lane & 7) ^ ((rho >> 1) & 7);
+        const int row = min(m0 + rho, M - 1);
+        a.xoff[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) * 2u + 16u * c;
     }
-    // weights: half-blocks of row tiles 2 j, 2 j + 1 of the workgroup
 #pragma unroll
     for (int i = 0; i < C::W_INSTR; ++i) {
         const int j = wave * C::W_INSTR + i;
-        const int t = min(a.tile0 + 2 * j + (lane >> 5), a.tile_last);
-        const u4* src = a.w + (static_cast<int64_t>(t) * a.G + g) * kBlockU4 + 32 * h + (lane & 31);
-        lds_dma<16>(src, slot + 16 * (C::X_U4 + 64 * j));
+        const int t = min(tile0 + 2 * j + (lane >> 5), tile_last);
+        a.woff[i] = static_cast<uint32_t>(t) * static_cast<uint32_t>(G) * 1024u + 16u * (lane & 31);
     }
-    // params of this wavefront's NT tiles, 4 bytes per lane with every lane active (no branch around the
-    // load): lane 16 t' + 8 kind + p of load i holds rows 2 p, 2 p + 1 of tile 4 i + t''s scales (kind 0)
-    // or zeros
-    {
-        const int wn = wave % WN;
-        const int kind = (lane >> 3) & 1, p = lane & 7;
-        const uint16_t* base = kind ? a.z16 : a.s16;
+    const int t = min(tile0 + wn * NT + (lane >> 3) % NT, tile_last);
+    a.poff = (static_cast<uint32_t>(t) * 16u * static_cast<uint32_t>(G) + 2u * (lane & 7)) * 2u;
+}
+
+// Issue the direct-to-LDS loads of stage `st` into `slot`. Every wavefront issues exactly LOADS
+// instructions, so each can wait for a stage with one vmcnt. Stage st = (group g, k half h) moves the
+// bases only: x by (128 g + 64 h) halves, the weights by block g and half h (g * 1024 + h * 512 bytes),
+// the scales and zeros by group g (16 g halves of every tile).
+template <int MT, int NT, int WM, int WN>
+__device__ __forceinline__ void issue_stage(uint32_t slot, const LdsGemmArgs<MT, NT, WM, WN>& a, int st, int wave) {
+    using C = LdsGemmCfg<MT, NT, WM, WN>;
+    const int g = st >> 1, h = st & 1;
+    const char* xb = a.x + (256 * g + 128 * h);
 #pragma unroll
-        for (int i = 0; i < C::P_INSTR; ++i) {
-            const int tile = min(a.tile0 + wn * NT + 4 * i + (lane >> 4), a.tile_last);
-            const uint16_t* src = base + static_cast<int64_t>(16) * tile * a.G + 16 * g + 2 * p;
-            lds_dma<4>(src, slot + 16 * (C::X_U4 + C::W_U4 + wave * NT * 4 + 16 * i));
-        }
-    }
+    for (int i = 0; i < C::X_INSTR; ++i) lds_dma<16>(xb, a.xoff[i], slot + 16 * 64 * (wave * C::X_INSTR + i));
+    const char* wb = a.w + (1024 * g + 512 * h);
+#pragma unroll
+    for (int i = 0; i < C::W_INSTR; ++i)
+        lds_dma<16>(wb, a.woff[i], slot + 16 * (C::X_U4 + 64 * (wave * C::W_INSTR + i)));
+    const uint32_t pslot = slot + 16 * (C::X_U4 + C::W_U4 + wave * 32);
+    lds_dma<4>(a.s16 + 32 * g, a.poff, pslot);         // scales [8 tiles][16 rows]
+    lds_dma<4>(a.z16 + 32 * g, a.poff, pslot + 256);   // zeros, the same order
 }
 
 // One stage's math from `slot`: two substeps of NT x MT MFMAs.
@@ -141,7 +160,7 @@ __device__ __forceinline__ void compute_stage(const u4* slot, f4 (&acc)[NT][MT],
     const int r = lane & 15, q = lane >> 4;
     const u4* xs = slot;
     const u4* ws = slot + C::X_U4;
-    const uint16_t* ps = reinterpret_cast<const uint16_t*>(slot + C::X_U4 + C::W_U4 + wave * NT * 4);
+    const uint16_t* ps = reinterpret_cast<const uint16_t*>(slot + C::X_U4 + C::W_U4 + wave * 32);  // [2][8][16]
     // lane (q, r) needs words s = q & 1 and 2 + (q & 1) of (kb = 2 h + (q >> 1), r): one ds_read2_b32
     uint32_t wv[NT][2];
     GroupQ pq[NT];
@@ -150,7 +169,7 @@ __device__ __forceinline__ void compute_stage(const u4* slot, f4 (&acc)[NT][MT],
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(ws + (wn * NT + t) * 32 + (q >> 1) * 16 + r) + (q & 1);
         wv[t][0] = wp[0];
         wv[t][1] = wp[2];
-        pq[t] = group_q(as_h1(ps[(2 * t) * 16 + r]), as_h1(ps[(2 * t + 1) * 16 + r]));
+        pq[t] = group_q(as_h1(ps[t * 16 + r]), as_h1(ps[128 + t * 16 + r]));
     }
     // both substeps' B fragments are read up front, so the second substep's LDS latency hides under the
     // first substep's MFMAs
@@ -161,7 +180,7 @@ __device__ __forceinline__ void compute_stage(const u4* slot, f4 (&acc)[NT][MT],
 #pragma unroll
         for (int b = 0; b < MT; ++b) {
             const int rho = wm * 16 * MT + 16 * b + r;
-            xb[j][b] = bitcast<h8>(xs[rho * 8 + (c ^ (rho & 7))]);
+            xb[j][b] = bitcast<h8>(xs[rho * 8 + (c ^ ((rho >> 1) & 7))]);
         }
     }
 #pragma unroll
@@ -199,13 +218,13 @@ __device__ __forceinline__ void ring_step(const u4* ring, uint32_t ring_addr, co
     }
     ring_barrier();
     if (i + R - 1 < nst)
-        issue_stage<MT, NT, WM, WN>(ring_addr + 16 * ((S + R - 1) % R) * C::SLOT_U4, a, st0 + i + R - 1, wave, lane);
+        issue_stage<MT, NT, WM, WN>(ring_addr + 16 * ((S + R - 1) % R) * C::SLOT_U4, a, st0 + i + R - 1, wave);
     compute_stage<MT, NT, WM, WN>(ring + S * C::SLOT_U4, acc, wave, wm, wn, lane, magic);
     __builtin_amdgcn_sched_barrier(0);  // one stage's registers at a time: no scheduling across steps
 }
 
 template <int MT, int NT, int WM, int WN, int R>
-__global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(LdsGemmCfg<MT, NT, WM, WN>::MIN_WAVES_PER_SIMD))) gemm_lds_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                                const h1* __restrict__ scales,
                                                                const h1* __restrict__ zeros, h1* __restrict__ y,
                                                                float* __restrict__ ws, int* __restrict__ locks, int M,
@@ -226,17 +245,13 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(const h1* __rest
     const int st0 = static_cast<int>(static_cast<int64_t>(split) * stages / splits);
     const int nst = static_cast<int>(static_cast<int64_t>(split + 1) * stages / splits) - st0;
 
+    const int m0 = mblk * C::BM, tile0 = nblk * (C::BN / 16);
     LdsGemmArgs<MT, NT, WM, WN> a;
-    a.x = x;
-    a.w = w;
-    a.s16 = reinterpret_cast<const uint16_t*>(scales);
-    a.z16 = reinterpret_cast<const uint16_t*>(zeros);
-    a.M = M;
-    a.K = K;
-    a.G = G;
-    a.m0 = mblk * C::BM;
-    a.tile0 = nblk * (C::BN / 16);
-    a.tile_last = tiles_n - 1;
+    a.x = reinterpret_cast<const char*>(x);
+    a.w = reinterpret_cast<const char*>(w);
+    a.s16 = reinterpret_cast<const char*>(scales);
+    a.z16 = reinterpret_cast<const char*>(zeros);
+    lds_gemm_offsets<MT, NT, WM, WN>(a, M, K, G, m0, tile0, tiles_n - 1, wave, wn, lane);
 
     const uint32_t magic = magic_reg();
     f4 acc[NT][MT];
@@ -249,7 +264,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(const h1* __rest
     const uint32_t ring_addr = static_cast<uint32_t>(reinterpret_cast<size_t>((lds_void*)ring));
 #pragma unroll
     for (int p = 0; p < R - 1; ++p)
-        if (p < nst) issue_stage<MT, NT, WM, WN>(ring_addr + 16 * p * C::SLOT_U4, a, st0 + p, wave, lane);
+        if (p < nst) issue_stage<MT, NT, WM, WN>(ring_addr + 16 * p * C::SLOT_U4, a, st0 + p, wave);
     for (int i = 0; i < nst; i += R) {
         ring_step<0, R>(ring, ring_addr, a, i, nst, st0, acc, wave, wm, wn, lane, magic);
         if (i + 1 < nst) ring_step<1, R>(ring, ring_addr, a, i + 1, nst, st0, acc, wave, wm, wn, lane, magic);
@@ -259,11 +274,11 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_lds_kernel(const h1* __rest
     }
 
     finish_unit<MT, NT, WM * WN>(acc, true, wave, lane, tid, splits, tile, unit, ws, locks, last_flag, y, M, N,
-                                 a.m0 + wm * 16 * MT, a.tile0 + wn * NT, tiles_n, act);
+                                 m0 + wm * 16 * MT, tile0 + wn * NT, tiles_n, act);
 }
 
 // Compiled configurations (MT, NT, WM, WN, ring slots).
-#define TW4_LDS_GEMM_CONFIGS(X) X(8, 4, 2, 4, 3) X(16, 4, 1, 4, 3) X(4, 4, 2, 4, 3) X(8, 4, 2, 2, 3)
+#define TW4_LDS_GEMM_CONFIGS(X) X(8, 4, 2, 4, 3) X(16, 4, 1, 4, 3) X(4, 4, 2, 4, 3) X(8, 4, 2, 2, 3) X(8, 8, 1, 4, 4) X(8, 4, 1, 4, 3)
 
 template <int MT, int NT, int WM, int WN, int R>
 int lds_gemm_launch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, float* ws, int* locks,
@@ -271,6 +286,9 @@ int lds_gemm_launch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, f
                     hipStream_t stream) {
     using C = LdsGemmCfg<MT, NT, WM, WN>;
     TW4_REQUIRE(N % 16 == 0, TW4_EINVAL, "gemm (stages 3): N %% 16 == 0 (N = %d)", N);
+    // the loads' per-lane byte offsets are 32-bit: x (M K 2 bytes) and the weights (N K / 2 bytes)
+    TW4_REQUIRE(static_cast<int64_t>(M) * K < (1LL << 31) && static_cast<int64_t>(N) * K < (1LL << 33), TW4_EINVAL,
+                "gemm (stages 3): M K < 2^31 and N K < 2^33 (M %d, N %d, K %d)", M, N, K);
     TW4_REQUIRE(reinterpret_cast<uintptr_t>(s) % 16 == 0 && reinterpret_cast<uintptr_t>(z) % 16 == 0, TW4_EINVAL,
                 "gemm (stages 3): scales and zeros must be 16-byte aligned");
     const int G = K >> 7, stages = 2 * G;

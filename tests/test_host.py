@@ -43,7 +43,11 @@ def test_library_exports_every_declared_symbol():
 def test_config_queries():
     dec, gemm = w4_hip.decode_configs(), w4_hip.gemm_configs()
     assert len(dec) >= 8 and all(len(c) == 3 and c[0] >= 1 and c[1] >= 1 for c in dec)
-    assert len(gemm) >= 8 and all(len(c) == 5 and c[3] in (1, 2) for c in gemm)
+    assert len(gemm) >= 8 and all(len(c) == 5 and c[4] in (0, 1, 2, 3) for c in gemm)
+    # warps_k: 1 or 2 wavefronts per K step (stages 0, 2), wavefronts along M (stages 3), or the
+    # wavefronts that split each unit's groups (stages 1, whose warps_n is the prefetch depth)
+    assert all(c[3] in ((4, 8) if c[4] == 1 else (1, 2)) for c in gemm)
+    assert {c[4] for c in gemm} == {0, 1, 2, 3}
     assert awq.DEFAULT_KERNEL[1:] in dec
     for m_max, cfg in awq.DEFAULT_GEMM:
         if cfg is not None and cfg[0] == "mma":
