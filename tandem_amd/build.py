@@ -35,7 +35,9 @@ def sources() -> list[str]:
 # Per-source flags. The decode kernels keep their MFMA accumulators in ordinary VGPRs instead of the
 # accumulation registers: no v_accvgpr moves around each quant group's MFMAs, and the persistent
 # decode kernel on Qwen3-8B gate_up at M = 8 measured 13.9 -> 13.4 us (the others level).
-SOURCE_FLAGS = {"tw4_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"tw4_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                # the GEMV's copy with its kernel arguments preloaded into SGPRs (13 dwords fit)
+                "tw4_gemv_kp.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _compile(src: str, obj: str) -> tuple[str, int, str]:

@@ -128,6 +128,21 @@ def test_gemv_silu_mul(ext):
                 check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
 
 
+def test_gemv_kp_is_the_gemv(ext):
+    """The GEMV compiled with its kernel arguments preloaded (tw4_gemv_kp) gives the plain GEMV's bits
+    at every compiled config, M = 1..4, plain and SwiGLU, and so its tolerance against the oracle."""
+    for k, n, inter in ((128, 24, False), (4096, 1000, False), (1024, 512, True)):
+        c = Case(k, n, seed=41, interleave=inter)
+        for m in range(1, 5):
+            x = c.x(m, seed=1300 + m)
+            xg = gpu(x)
+            ref = o.swiglu_reference(x, c.w_exact) if inter else o.linear(x, c.w_exact)
+            for cfg in DECODE_CONFIGS:
+                y = ext.w4_gemv_kp(xg, c.packed, c.s, c.zz, *cfg, int(inter))
+                assert torch.equal(y, ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg, int(inter))), (k, n, m, cfg)
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
+
+
 def test_gemv_mfma_every_config(ext):
     """The GEMV's arithmetic on the matrix cores (tw4_gemv_mfma), M = 1..4, every compiled config,
     plain and SwiGLU, at the GEMV's tolerance (exact q - z weights, like w4_gemv)."""

@@ -25,11 +25,16 @@ def test_noalloc_matches_workspace_entry_point():
     ext = w4_hip.load()
     buf, locks = w4_hip.workspace("cuda")
     rng = np.random.default_rng(77)
-    # (K, N, act, M of the first call, M of the second, config with splits)
+    # (K, N, act, M of the first call, M of the second, config with splits). A splits = 0 case must pick
+    # the same split count from either workspace size (the stages-3 launcher sizes it by the workspace),
+    # so the stages-3 case names its split.
     cases = [(4096, 6144, 0, 64, 33, (2, 1, 4, 2, 2, 4)),     # every tile split 4 ways
              (12288, 4096, 0, 64, 20, (2, 1, 4, 1, 2, 0)),    # the last partial wave split
              (4096, 2048, 1, 130, 17, (4, 2, 4, 1, 2, 2)),    # SwiGLU epilogue, split 2
              (4096, 1024, 0, 40, 24, (2, 2, 4, 1, 0, 0)),     # resident-x streaming form
+             (12288, 4096, 0, 32, 20, (2, 4, 1, 4, 1, 4)),    # x from L2 (stages 1), split 4
+             (4096, 2048, 1, 16, 9, (1, 2, 2, 8, 1, 0)),      # stages 1 at decode M, SwiGLU, auto split
+             (4096, 2048, 0, 300, 130, (8, 4, 4, 1, 3, 2)),   # both tiles through LDS (stages 3), split 2
              (1024, 512, 0, 300, 50, (8, 2, 4, 1, 2, 1))]     # no split
     for k, n, act, m1, m2, cfg in cases:
         packed, s, z, w = _weights(k, n, seed=k + n + act, interleave=bool(act))
