@@ -460,11 +460,13 @@ def test_decode_graph_replay(ext):
     x = gpu(c.x(4, seed=12))
     ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
     ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
+    ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         y1 = ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
         y2 = ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
+        y3 = ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)  # kernel arguments preloaded into SGPRs
     rng = np.random.default_rng(13)
     for _ in range(3):
         xn = rng.standard_normal((4, 4096)).astype(np.float16)
@@ -474,6 +476,10 @@ def test_decode_graph_replay(ext):
         ref = o.linear(xn, c.w_exact)
         check_close(y1, ref, 0.02, 0.01, "mma replay")
         check_close(y2, ref, 0.05, 0.02, "gemv replay")
+        check_close(y3, ref, 0.05, 0.02, "gemv_kp replay")
+        eager = ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(y3, eager), "gemv_kp: replay differs from the eager call"
 
 
 # ----------------------------------------------------------------- full Qwen3-8B shapes
