@@ -128,7 +128,7 @@ def kernel_of(awq, lin, m: int) -> str:
     """Which kernel W4Linear.forward runs for M (the same lookups as the forward)."""
     if m <= 16:
         kind = lin.decode_entry(m)
-        if kind[0] in ("gemv", "gemvk", "gemvm") and m > 4:
+        if kind[0] in ("gemv", "gemvm") and m > 4:
             kind = awq.DEFAULT_KERNEL
         return f"{kind[0]}{tuple(kind[1:])}"
     key = (lin.out_features, lin.in_features) + (("silu",) if lin.silu_mul else ())
@@ -561,7 +561,7 @@ def tune_main(argv=None) -> int:
     ap.add_argument("--model", default="qwen3-8b", choices=sorted(TUNE_MODELS))
     ap.add_argument("--projs", default="", help="comma list of projections (default: all)")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvk, gemvm, gemvn, mma, mmak, mmap, gemm, dense")
+    ap.add_argument("--kinds", default="gemv,mma", help="gemv, gemvm, gemvn, mma, mmak, mmap, gemm, dense")
     ap.add_argument("--splits", default="0,1,2,4,8")
     ap.add_argument("--per-cu", default="1,2,3,4", help="workgroups per CU of the persistent mma (kind mmap)")
     ap.add_argument("--act", action="store_true", help="time the SwiGLU epilogue (gate_up only)")
@@ -648,8 +648,6 @@ def tune_main(argv=None) -> int:
                     nw = (torch.rand(k, device=dev) + 0.5).half()
                     attempt(res, ("gemvn", *cfg),
                             [lambda w=w, c=cfg: ext.w4_decode_norm(x, r, nw, 1e-6, *w, 0, *c, act) for w in ws])
-                if "gemvk" in kinds and m <= 4:  # the GEMV with its kernel arguments preloaded
-                    attempt(res, ("gemvk", *cfg), [lambda w=w, c=cfg: ext.w4_gemv_kp(x, *w, *c, act) for w in ws])
                 if "gemvm" in kinds and m <= 4:
                     attempt(res, ("gemvm", *cfg), [lambda w=w, c=cfg: ext.w4_gemv_mfma(x, *w, *c, act) for w in ws])
                 if "mma" in kinds and m <= 64:

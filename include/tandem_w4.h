@@ -96,15 +96,6 @@ int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scale
                  const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                  int warps_k, int unroll, int ntile, int act, void* stream);
 
-/* tw4_gemv_act's kernel in a copy compiled with its kernel arguments preloaded into SGPRs (gfx950
- * loads them into user SGPRs before a wavefront starts): the same arithmetic, bits, configs, act and
- * limits; only the start of each wavefront differs. Small grids run faster with it (Qwen3-8B qkv and
- * o_proj at M = 1), large ones level or slower. No reference counterpart: an alternative kernel for
- * the (N, K, M) table entries of w4_gemv (python/tandem/layers/awq.py:136-160). */
-int tw4_gemv_kp(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
-                const uint16_t* zeros, uint16_t* y, int M, int N, int K,
-                int warps_k, int unroll, int ntile, int act, void* stream);
-
 /* The GEMV's arithmetic on the matrix cores, 1 <= M <= 4: raw magic halves (1024 + q) times x' on
  * v_mfma_f32_16x16x32_f16, the bias and the zero point in the accumulator's start value, the scale
  * per group; exact (q - z) weights like tw4_gemv (so the GEMV's tolerance). Same configs, act and

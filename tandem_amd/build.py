@@ -32,12 +32,16 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-# Per-source flags. The decode kernels keep their MFMA accumulators in ordinary VGPRs instead of the
-# accumulation registers: no v_accvgpr moves around each quant group's MFMAs, and the persistent
-# decode kernel on Qwen3-8B gate_up at M = 8 measured 13.9 -> 13.4 us (the others level).
-SOURCE_FLAGS = {"tw4_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-                # the GEMV's copy with its kernel arguments preloaded into SGPRs (13 dwords fit)
-                "tw4_gemv_kp.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+# Per-source flags for the decode kernels (tw4_decode.hip).
+# - The MFMA accumulators sit in ordinary VGPRs instead of the accumulation registers: no
+#   v_accvgpr moves around each quant group's MFMAs. The persistent decode kernel on Qwen3-8B
+#   gate_up at M = 8 measured 13.9 -> 13.4 us (the others level).
+# - The first 16 kernel-argument dwords are preloaded into user SGPRs before a wavefront starts, so
+#   its first instructions do not wait on an s_load of the arguments. This shortens the start of
+#   the small decode grids: the GEMV on Qwen3-8B qkv at M = 1 measured 4.74 -> 4.39 us, the
+#   matrix-core kernels 1.5-3 % and the GEMV on the matrix cores 3-6 % at M = 2-16. gate_up's grid
+#   of 1536 workgroups is level.
+SOURCE_FLAGS = {"tw4_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _compile(src: str, obj: str) -> tuple[str, int, str]:

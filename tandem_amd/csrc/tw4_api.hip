@@ -11,7 +11,6 @@
 int tw4_gemm_prepare_device(int dev);    // tw4_gemm.hip
 int tw4_decode_prepare_device(int dev);  // tw4_decode.hip
 int tw4_noalloc_prepare_device(int dev); // tw4_noalloc.hip
-int tw4_gemv_kp_prepare_device(int dev);  // tw4_gemv_kp.hip
 
 namespace tw4host {
 
@@ -57,7 +56,6 @@ extern "C" int tw4_init(int device) {
     int rc = tw4_gemm_prepare_device(device);
     if (rc == TW4_OK) rc = tw4_decode_prepare_device(device);
     if (rc == TW4_OK) rc = tw4_noalloc_prepare_device(device);
-    if (rc == TW4_OK) rc = tw4_gemv_kp_prepare_device(device);
     if (current != device) {
         e = hipSetDevice(current);
         if (e != hipSuccess && rc == TW4_OK) return tw4host::hip_fail(e, "init: restore device");

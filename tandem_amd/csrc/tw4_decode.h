@@ -1,6 +1,6 @@
-// Decode kernels shared by tw4_decode.hip and tw4_gemv_kp.hip: the streaming helpers, x staging, the fused
+// Building blocks of the decode kernels (tw4_decode.hip): the streaming helpers, x staging, the fused
 // norm prologue and the vector-ALU GEMV (its launcher gemv_dispatch too), and the compiled decode
-// configurations. Everything here is a template or inline, so both translation units can include it.
+// configurations. Everything here is a template or inline.
 //
 // Decode kernels, M <= 64: y[M, N] = x[M, K] @ dequant(W)^T, bound by streaming the int4 weights.
 //
@@ -457,9 +457,7 @@ __device__ __forceinline__ void gemv_chunk(const WeightSet<U, NT>& cur, WeightSe
     }
 }
 
-// KP: the copy compiled with the kernel arguments preloaded into SGPRs (tw4_gemv_kp.hip); the code is
-// the same, the parameter keeps the two copies' symbols apart.
-template <int M, int WK, int U, int NT, bool NORM, bool KP = false>
+template <int M, int WK, int U, int NT, bool NORM>
 __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                       const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                       h1* __restrict__ y, int N, int K, int act, NormIn nin) {
@@ -575,9 +573,9 @@ constexpr int kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr int kXLdsLimit = 80 * 1024;    // mma keeps x in LDS up to this size (M = 8 at K = 4096)
 constexpr int kXLdsBig = 136 * 1024;     // ... and up to this one when the grid has at most one workgroup per CU
 
-// Launch the vector-ALU GEMV (M <= 4) of one compiled configuration; KP picks the kernel-argument-
-// preloading copy. LDS beyond 64 KB needs the kernel's hipFuncSetAttribute (tw4_init / the first call).
-template <int M, bool NORM, bool KP = false>
+// Launch the vector-ALU GEMV (M <= 4) of one compiled configuration. LDS beyond 64 KB needs the
+// kernel's hipFuncSetAttribute (tw4_init / the first call).
+template <int M, bool NORM>
 int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
                   int act, const NormIn& nin, hipStream_t st) {
     const int tiles = (N + 15) >> 4;
@@ -587,7 +585,7 @@ int gemv_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int
             16 * static_cast<size_t>(decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, T), NORM).total); \
         TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
                     "gemv: x [%d, %d] does not fit in LDS (use mma)", M, K);                                 \
-        gemv_kernel<M, WK, U, T, NORM, KP><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act, nin); \
+        gemv_kernel<M, WK, U, T, NORM><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act, nin); \
         TW4_LAUNCH_CHECK("gemv: launch");                                                                    \
         return TW4_OK;                                                                                       \
     }

@@ -142,8 +142,6 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 # `python bench.py tune` sweeps on the GPU:
 #   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4 (with the SwiGLU epilogue too: the
 #                                      reference's SwiGLU gate_up always takes "mma")
-#   ("gemvk", warps_k, unroll, ntile)  the same GEMV compiled with its kernel arguments preloaded into
-#                                      SGPRs (tw4_gemv_kp: a faster wavefront start on small grids), M <= 4
 #   ("gemvm", warps_k, unroll, ntile)  the GEMV's arithmetic (exact q - z, scale per group) on the
 #                                      matrix cores, M <= 4
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
@@ -357,8 +355,6 @@ class W4Linear(nn.Module):
                     return self._gemm(ext, x, cfg)
                 if kind == "gemv" and m <= 4:  # with the SwiGLU epilogue too (tw4_gemv_act)
                     return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
-                if kind == "gemvk" and m <= 4:  # the GEMV with its kernel arguments preloaded (small grids)
-                    return ext.w4_gemv_kp(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
                 if kind == "gemvm" and m <= 4:  # the GEMV's arithmetic on the matrix cores
                     return ext.w4_gemv_mfma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
                 if kind == "mmak":  # the matrix-core decode kernel with K split over workgroups
@@ -367,7 +363,7 @@ class W4Linear(nn.Module):
                                              int(self.silu_mul))
                 if kind == "mmap":  # the matrix-core decode kernel, persistent workgroups
                     return ext.w4_mma_persist(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
-                if kind != "mma":  # gemv / gemvk / gemvm past M = 4
+                if kind != "mma":  # gemv / gemvm past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
         elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul

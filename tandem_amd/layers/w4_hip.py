@@ -45,7 +45,6 @@ _SIGNATURES = {
     "tw4_gemv": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_act": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_mfma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
-    "tw4_gemv_kp": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma_splitk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "tw4_mma_persist": ([_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -185,20 +184,6 @@ class W4Extension:
         with torch.cuda.device(x.device):
             check(self.lib.tw4_gemv_mfma(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
                                          int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
-        return y
-
-    def w4_gemv_kp(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int = 0) -> torch.Tensor:
-        """w4_gemv's kernel compiled with its kernel arguments preloaded into SGPRs (tw4_gemv_kp; no reference
-        counterpart): the same results, a faster wavefront start on small grids. M <= 4."""
-        m, n, k = check_operands("w4_gemv_kp", x, w, s, z)
-        if not 1 <= m <= 4:
-            raise RuntimeError("w4_gemv_kp: M <= 4 (larger M: w4_mma)")
-        if act not in (0, 1) or (act and n % 16):
-            raise RuntimeError("w4_gemv_kp: act 0, or 1 (SwiGLU) with N % 16 == 0")
-        y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)
-        with torch.cuda.device(x.device):
-            check(self.lib.tw4_gemv_kp(_ptr(x), _ptr(w), _ptr(s), _ptr(z), _ptr(y), m, n, k,
-                                       int(warps_k), int(unroll), int(ntile), int(act), _stream(x)))
         return y
 
     def w4_decode_norm(self, x, residual, norm_weight, eps: float, w, s, z, kind: int, warps_k: int, unroll: int,

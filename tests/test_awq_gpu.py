@@ -128,21 +128,6 @@ def test_gemv_silu_mul(ext):
                 check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
 
 
-def test_gemv_kp_is_the_gemv(ext):
-    """The GEMV compiled with its kernel arguments preloaded (tw4_gemv_kp) gives the plain GEMV's bits
-    at every compiled config, M = 1..4, plain and SwiGLU, and so its tolerance against the oracle."""
-    for k, n, inter in ((128, 24, False), (4096, 1000, False), (1024, 512, True)):
-        c = Case(k, n, seed=41, interleave=inter)
-        for m in range(1, 5):
-            x = c.x(m, seed=1300 + m)
-            xg = gpu(x)
-            ref = o.swiglu_reference(x, c.w_exact) if inter else o.linear(x, c.w_exact)
-            for cfg in DECODE_CONFIGS:
-                y = ext.w4_gemv_kp(xg, c.packed, c.s, c.zz, *cfg, int(inter))
-                assert torch.equal(y, ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg, int(inter))), (k, n, m, cfg)
-                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
-
-
 def test_gemv_mfma_every_config(ext):
     """The GEMV's arithmetic on the matrix cores (tw4_gemv_mfma), M = 1..4, every compiled config,
     plain and SwiGLU, at the GEMV's tolerance (exact q - z weights, like w4_gemv)."""
@@ -460,13 +445,13 @@ def test_decode_graph_replay(ext):
     x = gpu(c.x(4, seed=12))
     ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
     ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
-    ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)
+    ext.w4_gemv_mfma(x, c.packed, c.s, c.zz, 8, 2, 1)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         y1 = ext.w4_mma(x, c.packed, c.s, c.zz, 4, 2, 1, 0)
         y2 = ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
-        y3 = ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)  # kernel arguments preloaded into SGPRs
+        y3 = ext.w4_gemv_mfma(x, c.packed, c.s, c.zz, 8, 2, 1)
     rng = np.random.default_rng(13)
     for _ in range(3):
         xn = rng.standard_normal((4, 4096)).astype(np.float16)
@@ -476,10 +461,10 @@ def test_decode_graph_replay(ext):
         ref = o.linear(xn, c.w_exact)
         check_close(y1, ref, 0.02, 0.01, "mma replay")
         check_close(y2, ref, 0.05, 0.02, "gemv replay")
-        check_close(y3, ref, 0.05, 0.02, "gemv_kp replay")
-        eager = ext.w4_gemv_kp(x, c.packed, c.s, c.zz, 8, 2, 1)
+        check_close(y3, ref, 0.05, 0.02, "gemv_mfma replay")
+        eager = ext.w4_gemv(x, c.packed, c.s, c.zz, 4, 2, 1)
         torch.cuda.synchronize()
-        assert torch.equal(y3, eager), "gemv_kp: replay differs from the eager call"
+        assert torch.equal(y2, eager), "gemv: replay differs from the eager call"
 
 
 # ----------------------------------------------------------------- full Qwen3-8B shapes

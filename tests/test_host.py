@@ -82,9 +82,6 @@ def test_argument_errors_return_before_launch():
         (lambda: lib.tw4_gemv(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 64, 65536 + 128, 1, 4, 1, None), "K <= 65536"),
         (lambda: lib.tw4_gemv_act(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 24, 128, 4, 2, 1, 1, None),
          "SwiGLU"),
-        (lambda: lib.tw4_gemv_kp(_fake(), _fake(), _fake(), _fake(), _fake(), 5, 64, 128, 4, 2, 1, 0, None), "M <= 4"),
-        (lambda: lib.tw4_gemv_kp(_fake(), _fake(), _fake(), _fake(), _fake(), 1, 24, 128, 4, 2, 1, 1, None),
-         "SwiGLU"),
         (lambda: lib.tw4_mma(_fake(), _fake(), _fake(), _fake(), _fake(), 65, 64, 128, 4, 2, 1, 0, None), "M <= 64"),
         (lambda: lib.tw4_rms_norm(_fake(), _fake(), _fake(), 1, 1000, 1e-6, None), "K % 512"),
         (lambda: lib.tw4_rms_norm(_fake(), _fake(), _fake(), 1, 16384, 1e-6, None), "K <= 8192"),
@@ -242,8 +239,8 @@ def test_tables_are_well_formed():
             elif cfg[0] == "mmap":  # a compiled decode config, 1 .. 8 workgroups per CU, x in LDS
                 assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 1 <= cfg[4] <= 8
                 assert m * (2 * k + 16) <= 136 * 1024  # past 80 KB only for grids of at most one per CU
-            else:  # a compiled decode config; gemv / gemvk / gemvm only where they run (M <= 4)
-                assert cfg[0] in ("gemv", "gemvk", "gemvm", "mma") and tuple(cfg[1:]) in decode
+            else:  # a compiled decode config; gemv / gemvm only where they run (M <= 4)
+                assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
                 assert cfg[0] == "mma" or m <= 4
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
         m_maxes = [m for m, _ in ladder]
