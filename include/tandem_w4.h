@@ -175,7 +175,10 @@ int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* sc
  *           the number of wavefronts along M (BM = 16 mt warps_k, BN = 16 nt warps_n); N % 16 == 0,
  *           scales and zeros 16-byte aligned; splits = 0 picks enough K splits to fill the GPU
  *   splits  0: split only the last, partial wave of tiles along K; 1: no split; s > 1: every
- *           tile split s ways
+ *           tile split s ways. The partial-wave rule counts tile waves, not bytes: where the whole
+ *           grid fits in one wave it splits every tile, and on a bandwidth-bound shape the fp32
+ *           partials can cost more than the split saves (Qwen3-8B gate_up at M = 32 with
+ *           (2, 1, 4, 2, 2, 0) moved 1.64x its algorithmic bytes). The gfx950 tables name the split.
  * ws (fp32, ws_floats) and locks (int32, n_locks, zero before the first call) are the split-K
  * workspace; the kernel returns every counter to zero, so graph replays stay correct. Calls
  * that share a workspace must not overlap.
