@@ -556,12 +556,13 @@ def test_w4linear_gemm_switch_off(monkeypatch):
 def test_w4linear_qwen3_8b_tables(proj, silu):
     """W4Linear at the real Qwen3-8B shapes through the gfx950 tables, across the M ranges where
     the tables switch kernels (gemv, gemvm, mma and its split-K and persistent forms, the GEMM with
-    and without split-K): every M of the benchmark's decode sweep and its M = 24 / 32 / 64 entries."""
+    and without split-K, the x-from-L2 and resident-x kernels at M = 17 .. 24): every M of the
+    benchmark's decode sweep, its M = 24 / 32 / 64 entries and a point inside each ladder rung."""
     k, n = QWEN3_8B[proj]
     layer, c = _layer(k, n, seed=SEEDS[proj] + 10, silu_mul=silu)
     assert layer.kernels is awq.W4_KERNELS[awq.GFX950] and layer.gemm_kernels is awq.W4_GEMM_KERNELS[awq.GFX950]
     rng = np.random.default_rng(23)
-    for m in (1, 2, 4, 5, 7, 8, 12, 16, 24, 32, 48, 64, 130):
+    for m in (1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 20, 24, 32, 48, 64, 96, 130):
         x = rng.standard_normal((m, k)).astype(np.float16)
         y = layer(gpu(x))
         if silu:
