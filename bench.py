@@ -25,7 +25,9 @@ value = whole-step algorithmic HBM bytes / time (GB/s), with the per-call byte c
                 (the reference's CPU-runnable config) and on one Qwen3-8B layer at the benchmark's M:
                 fp16 and fp32 products, and the matmul alone on a pre-dequantized weight
   detail        per projection and M in {1, 8, 32}: us/call, GB/s, % of peak, TFLOP/s, the kernel
-                that ran, and at M = 32 the dequantize + torch.matmul comparator
+                that ran, its parity against dequantize + torch.matmul on the same x (max |err| /
+                max |ref| and cosine; parity_vs_dense holds the worst of them), and at M = 32 that
+                comparator's time
   full_stack    the whole decode step of the linears plus the fp16 lm_head (4096 x 151936, through
                 layers/gemv16.py's table: the HIP fp16 GEMV where it has an entry, else F.linear),
                 M in {1, 8, 32}: us per step and GB/s
@@ -126,16 +128,18 @@ def time_graph(torch, graph, stream, reps: int) -> float:
 
 def kernel_of(awq, lin, m: int) -> str:
     """Which kernel W4Linear.forward runs for M (the same lookups as the forward)."""
-    if m <= 16:
-        kind = lin.decode_entry(m)
-        if kind[0] in ("gemv", "gemvm") and m > 4:
-            kind = awq.DEFAULT_KERNEL
-        return f"{kind[0]}{tuple(kind[1:])}"
-    key = (lin.out_features, lin.in_features) + (("silu",) if lin.silu_mul else ())
-    cfg = awq.pick_gemm(lin.gemm_kernels.get(key, awq.DEFAULT_GEMM), m)
-    if cfg is None or not awq.FUSED_GEMM:
-        return "dequant+matmul"
-    return f"mma{tuple(cfg[1:])}" if cfg[0] == "mma" else f"gemm{cfg}"
+    return lin.kernel_for(m)
+
+
+def parity_vs_dense(torch, lin, x) -> dict:
+    """The fused output against the dequantize-then-fp16-matmul path on the same x (HIP dequant, then
+    torch.matmul, as the reference's bench compares, benchmarks/bench_w4_gemm.py:84-92): max_rel =
+    max |fused - dense| / max |dense| and the cosine similarity, in float64; outside any timed region."""
+    a = lin(x).double()
+    b = lin._dense(x).double()
+    rel = float((a - b).abs().max() / b.abs().max().clamp_min(1e-6))
+    cos = float((a * b).sum() / (a.norm() * b.norm()).clamp_min(1e-30))
+    return {"max_rel_vs_dense": float(f"{rel:.3g}"), "cos_vs_dense": round(cos, 7)}
 
 
 # ------------------------------------------------------------------------------------ sweep
@@ -280,7 +284,7 @@ def cpu_baseline(m: int) -> dict:
     from oracle import torch_fallback as tf
 
     cores = len(os.sched_getaffinity(0))
-    threads = min(cores, 16)  # one GPU's share of the box's host cores
+    threads = cores  # every core this process may run on
     torch.set_num_threads(threads)
 
     def median_s(fn) -> float:
@@ -472,7 +476,8 @@ def main(argv=None) -> int:
                 b, f = call_bytes(mm, k, n), 2 * mm * k * n
                 rec = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                        "pct_hbm_peak": round(b / us / 1e3 / HBM_PEAK_GBS * 100, 1),
-                       "TFLOPs": round(f / us / 1e6, 2), "kernel": kernel_of(awq, layers[0][proj], mm)}
+                       "TFLOPs": round(f / us / 1e6, 2), "kernel": kernel_of(awq, layers[0][proj], mm),
+                       **parity_vs_dense(torch, layers[0][proj], xd[k])}
                 if mm == 32:  # the dequantize-then-fp16-GEMM comparator (HIP dequant + torch.matmul)
                     dg = graph_of(torch, lambda: [layer[proj]._dense(xd[k]) for layer in layers[:8]], stream)
                     rec["dequant_matmul_us"] = round(time_graph(torch, dg, stream, reps=10) / 8 * 1e6, 2)
@@ -522,7 +527,12 @@ def main(argv=None) -> int:
                    "step_bytes": step_bytes, "step_flops": step_flops},
         "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
         "us_per_layer": round(step_s / a.layers * 1e6, 2),
-        "roofline": roofline, "cpu_baseline": cpu, "detail": detail, "full_stack": full, "decode_step": step,
+        "roofline": roofline, "cpu_baseline": cpu,
+        "parity_vs_dense": {"worst_max_rel": max((r["max_rel_vs_dense"] for r in detail.values()), default=None),
+                            "min_cos": min((r["cos_vs_dense"] for r in detail.values()), default=None),
+                            "what": "every detail cell's fused output against HIP dequant + torch.matmul (fp16) "
+                                    "on the same x"},
+        "detail": detail, "full_stack": full, "decode_step": step,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(line), flush=True)

@@ -181,9 +181,15 @@ int tw4_mma_persist(const uint16_t* x, const int32_t* packed, const uint16_t* sc
  *           (2, 1, 4, 2, 2, 0) moved 1.64x its algorithmic bytes). The gfx950 tables name the split.
  * ws (fp32, ws_floats) and locks (int32, n_locks, zero before the first call) are the split-K
  * workspace; the kernel returns every counter to zero, so graph replays stay correct. Calls
- * that share a workspace must not overlap.
+ * that share a workspace must not overlap. splits = 0 chooses its split from the tiles and the
+ * CU count within a fixed budget of TW4_AUTO_SPLIT_FLOATS partials and TW4_AUTO_SPLIT_COUNTERS
+ * counters (the default workspace's size), never from ws_floats / n_locks: a given config and
+ * shape always runs the same split and gives the same bits, and a workspace smaller than that
+ * split needs is refused with TW4_ESPACE.
  * Replaces w4_gemm / gemm_launch (python/tandem/csrc/w4_gemv.cu:312-566, 650-683) and the
  * workspace contract of python/tandem/layers/w4_cuda.py:24-41. */
+#define TW4_AUTO_SPLIT_FLOATS (1LL << 23)
+#define TW4_AUTO_SPLIT_COUNTERS (1 << 15)
 int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
              const uint16_t* zeros, uint16_t* y, float* ws, int32_t* locks,
              int64_t ws_floats, int64_t n_locks, int M, int N, int K,
@@ -192,17 +198,18 @@ int tw4_gemm(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
 
 /* tw4_gemm without a caller workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
- * reference: its w4_gemm always takes the Python-owned workspace (python/tandem/layers/w4_cuda.py:24-41).
- * Same kernels, arguments (minus ws / locks / sizes), results and errors as tw4_gemm; the split-K
- * partial sums and tile counters live in a static device array of the library, one per GPU, of
- * TW4_NOALLOC_FLOATS fp32 values and TW4_NOALLOC_COUNTERS int32 counters, held until the process ends.
- * A call whose split-K needs more is refused with TW4_ESPACE (splits = 0 only splits within the
- * limit). The function allocates nothing and never synchronizes. tw4_init(device) sets the array up
+ * reference. Same kernels, arguments (minus ws / locks / sizes), results and errors as tw4_gemm
+ * called with a workspace of TW4_NOALLOC_FLOATS fp32 values and TW4_NOALLOC_COUNTERS counters, which
+ * is the default workspace's size and the budget splits = 0 chooses within: every call tw4_gemm
+ * accepts with that workspace runs the same split here and gives the same bits. The split-K
+ * partial sums and tile counters live in a static device array of the library, one per GPU, held
+ * until the process ends. A call whose split-K needs more is refused with TW4_ESPACE. The function
+ * allocates nothing and never synchronizes. tw4_init(device) sets the array up
  * (its address and cleared counters); without it the first call on a device does, and then must not
  * be under graph capture (TW4_EINVAL). All calls on one GPU share the array: calls that overlap on a
  * GPU (other streams or threads) race and must be serialized by the caller. */
-#define TW4_NOALLOC_FLOATS (1LL << 21)
-#define TW4_NOALLOC_COUNTERS 16384
+#define TW4_NOALLOC_FLOATS TW4_AUTO_SPLIT_FLOATS
+#define TW4_NOALLOC_COUNTERS TW4_AUTO_SPLIT_COUNTERS
 int tw4_gemm_noalloc(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
                      const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                      int mt, int nt, int warps_n, int warps_k, int stages, int splits, int act,

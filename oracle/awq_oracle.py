@@ -11,12 +11,14 @@ relative to its repository root):
                                                                     tests/test_awq.py:17-29
     dequant                    fp16_rne((q - z) * s), [N, K]       python/tandem/layers/awq.py:89-133
     dequant_exact              (q - z) * s without rounding        tests/test_awq.py:32-38
+    dequant_exact_rows         the same for selected output        python/tandem/layers/awq.py:38-46
+                               features (sampled full-size checks)
     interleave_gate_up         16-row gate/up tiles                python/tandem/layers/awq.py:71-75
     deinterleave_gate_up       its inverse (w4_dequant's           python/tandem/layers/awq.py:114-118
                                DEINTERLEAVE destination rows)
     linear                     x @ w^T in float64 (the dequantize-  python/tandem/layers/awq.py:282-285
                                then-matmul path, at high precision)
-    silu_and_mul               silu(gate) * up on [gate | up]      python/tandem/layers/awq.py:78-86
+    silu / silu_and_mul        silu(gate) * up on [gate | up]      python/tandem/layers/awq.py:78-86
     swiglu_reference           float32 SwiGLU on fp16-rounded      tests/test_awq.py:80-84
                                weights
     random_awq                 the reference tests' input recipe   tests/test_awq.py:32-38
@@ -27,11 +29,12 @@ relative to its repository root):
 
 What pins each function (tests/test_oracle.py): known-answer words and the test packer's inverse
 for the nibble order; brute force over every (q, z) pair against exact rational arithmetic for the
-dequantization; closed forms for the interleave; explicit loops for the matmul; closed forms
-(constant rows, eps-dominated rows) and explicit loops for the norms; and planted mistakes
-(swapped orders, double rounding, transposed operands, a dropped eps or residual) that those checks
-must reject.
-No function of this module is "parity unpinned".
+dequantization, and the committed fixture plus single-entry rationals for the row-sampled form;
+closed forms for the interleave and SwiGLU; explicit loops for the matmul; the recipe's ranges,
+shapes and packing for random_awq; closed forms (constant rows, eps-dominated rows) and explicit
+loops for the norms; and planted mistakes (swapped orders, double rounding, transposed operands, a
+dropped eps or residual) that those checks must reject. Every function of this module has such a
+pin: none is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -156,16 +159,6 @@ def swiglu_reference(x: np.ndarray, w_exact: np.ndarray) -> np.ndarray:
     """SwiGLU reference on the fp16-rounded weights the kernels use (tests/test_awq.py:80-84):
     x [M, K], w_exact [2I, K] in [gate | up] row order -> [M, I]."""
     return silu_and_mul(linear(x, np.asarray(w_exact, dtype=np.float32).astype(np.float16)))
-
-
-def dequant_then_linear(x: np.ndarray, qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray,
-                        group: int = GROUP, out_dtype=np.float16, matmul_dtype=np.float32) -> np.ndarray:
-    """The reference's fallback, restated for the CPU: dequantize every call, then one matmul
-    (python/tandem/layers/awq.py:284-285). ``matmul_dtype`` float32 is numpy's BLAS path; the
-    result is rounded to ``out_dtype`` like F.linear's fp16 output."""
-    w = dequant(qweight, qzeros, scales, group)
-    y = np.asarray(x, dtype=matmul_dtype) @ w.astype(matmul_dtype).T
-    return y.astype(out_dtype)
 
 
 def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

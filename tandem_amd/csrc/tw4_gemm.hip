@@ -487,12 +487,20 @@ int gemm_launch(int dev, int index, const h1* x, const u4* w, const h1* s, const
         const int rem = tiles % slots;
         double best = 1.0;  // s = 1: one more wave of whole tiles, in units of one tile's time
         for (int c = 2; c <= 8 && c <= steps && rem > 0; ++c) {
-            if (static_cast<int64_t>(rem) * c * tile_floats > ws_floats || rem > n_locks) break;
+            // the budget is the default workspace, not the caller's, so the choice (and the bits) never
+            // depend on the workspace size; one too small for it is refused below
+            if (static_cast<int64_t>(rem) * c * tile_floats > TW4_AUTO_SPLIT_FLOATS || rem > TW4_AUTO_SPLIT_COUNTERS)
+                break;
             // the split wave's time in tile units, plus a fix-up cost per extra split
             const double t = static_cast<double>((static_cast<int64_t>(rem) * c + slots - 1) / slots) / c + 0.02 * c;
             if (t < best) best = t, sp = c;
         }
-        if (sp > 1) dp = tiles - rem;
+        if (sp > 1) {
+            dp = tiles - rem;
+            TW4_REQUIRE(ws && locks, TW4_EINVAL, "gemm: split-K needs a workspace and counters");
+            TW4_REQUIRE(static_cast<int64_t>(rem) * sp * tile_floats <= ws_floats && rem <= n_locks, TW4_ESPACE,
+                        "gemm: split-K workspace too small for %d tiles x %d splits", rem, sp);
+        }
     } else if (splits > 1) {
         TW4_REQUIRE(splits <= steps, TW4_EINVAL, "gemm: splits %d > K steps %d", splits, steps);
         TW4_REQUIRE(static_cast<int64_t>(tiles) * splits * tile_floats <= ws_floats && tiles <= n_locks, TW4_ESPACE,

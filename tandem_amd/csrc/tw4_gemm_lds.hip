@@ -302,10 +302,11 @@ int lds_gemm_launch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, f
     TW4_REQUIRE(tiles64 < (1LL << 30), TW4_EINVAL, "gemm: too many tiles (%lld)", static_cast<long long>(tiles64));
     const int tiles = static_cast<int>(tiles64);
     int sp = splits;
-    if (sp == 0) {  // enough units to fill the GPU once, within the workspace
+    if (sp == 0) {  // enough units to fill the GPU once, within the default workspace (never the caller's)
         sp = 1;
         while (static_cast<int64_t>(tiles) * sp < cus && 2 * (sp + 1) <= stages &&
-               static_cast<int64_t>(tiles) * (sp + 1) * C::BM * C::BN <= ws_floats && tiles <= n_locks)
+               static_cast<int64_t>(tiles) * (sp + 1) * C::BM * C::BN <= TW4_AUTO_SPLIT_FLOATS &&
+               tiles <= TW4_AUTO_SPLIT_COUNTERS)
             ++sp;
     }
     TW4_REQUIRE(sp >= 1 && sp <= stages, TW4_EINVAL, "gemm: splits %d for %d stages", sp, stages);

@@ -235,10 +235,11 @@ int mid_launch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, float*
     TW4_REQUIRE(static_cast<int64_t>(M) * K < (1LL << 30), TW4_EINVAL, "gemm (stages 1): M K < 2^30");
     constexpr int64_t kPart = static_cast<int64_t>(NT) * MT * 256;  // floats of one unit's partial
     int sp = splits;
-    if (sp == 0) {  // enough units to give every CU one, within the workspace
+    if (sp == 0) {  // enough units to give every CU one, within the default workspace (never the caller's)
         sp = 1;
         while (static_cast<int64_t>(groups) * sp < cus && sp < G &&
-               static_cast<int64_t>(groups) * (sp + 1) * kPart <= ws_floats && groups <= n_locks)
+               static_cast<int64_t>(groups) * (sp + 1) * kPart <= TW4_AUTO_SPLIT_FLOATS &&
+               groups <= TW4_AUTO_SPLIT_COUNTERS)
             ++sp;
     }
     TW4_REQUIRE(sp >= 1 && sp <= G, TW4_EINVAL, "gemm (stages 1): splits %d for %d groups", sp, G);

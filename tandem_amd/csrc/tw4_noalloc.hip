@@ -19,7 +19,7 @@
 namespace tw4 {
 
 constexpr int kScratchLocks = TW4_NOALLOC_COUNTERS;       // tiles a split call may use
-constexpr int64_t kScratchFloats = TW4_NOALLOC_FLOATS;    // fp32 partials (8 MiB)
+constexpr int64_t kScratchFloats = TW4_NOALLOC_FLOATS;    // fp32 partials (32 MiB, the default workspace)
 constexpr int64_t kScratchLockBytes = kScratchLocks * 4;
 constexpr int64_t kScratchBytes = kScratchLockBytes + kScratchFloats * 4;
 static_assert(kScratchLockBytes % 256 == 0, "partials stay 256-byte aligned");

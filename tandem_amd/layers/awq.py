@@ -206,8 +206,9 @@ def _hip_ok(x: torch.Tensor) -> bool:
 
 
 def _gemm_ok(x: torch.Tensor) -> bool:
-    """The M > 16 GEMM (python/tandem/layers/awq.py:201-203)."""
-    return FUSED_GEMM and x.is_cuda and _aligned(x) and x.shape[0] > 16
+    """The M > 16 GEMM (python/tandem/layers/awq.py:201-203), within its M x K < 2^31 limit (the
+    reference's w4_gemm check, csrc/w4_gemv.cu:661): larger inputs take dequantize + matmul."""
+    return FUSED_GEMM and x.is_cuda and _aligned(x) and x.shape[0] > 16 and x.shape[0] * x.shape[1] < 1 << 31
 
 
 def _table(tables: dict, device_name: str | None, device: torch.device) -> dict:
@@ -290,6 +291,22 @@ class W4Linear(nn.Module):
     def _gemm(self, ext, x: torch.Tensor, cfg) -> torch.Tensor:
         buf, locks = w4_hip.workspace(x.device)
         return ext.w4_gemm(x, self.packed, self.scales, self.zeros, buf, locks, *cfg, int(self.silu_mul))
+
+    def kernel_for(self, m: int) -> str:
+        """The kernel forward runs for a 16-byte aligned fp16 x of M rows on the GPU, by the same
+        lookups as forward: e.g. "gemv(4, 2, 1)", "gemm(2, 1, 4, 2, 2, 4)" or "dequant+matmul"."""
+        if m == 0:
+            return "empty"
+        if m <= 16:
+            kind, *cfg = self.decode_entry(m)
+            if kind not in ("gemm", "mmak", "mmap", "mma") and not (kind in ("gemv", "gemvm") and m <= 4):
+                kind, *cfg = DEFAULT_KERNEL
+            return f"{kind}{tuple(cfg)}"
+        key = (self.out_features, self.in_features) + (("silu",) if self.silu_mul else ())
+        cfg = pick_gemm(self.gemm_kernels.get(key, DEFAULT_GEMM), m)
+        if not FUSED_GEMM or cfg is None or m * self.in_features >= 1 << 31 or (cfg[0] == "mma" and m > 64):
+            return "dequant+matmul"
+        return f"mma{tuple(cfg[1:])}" if cfg[0] == "mma" else f"gemm{tuple(cfg)}"
 
     def decode_entry(self, m: int) -> W4Kernel:
         """The table entry forward uses at 1 <= M <= 16."""

@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import awq_oracle as o
+from parity import check_close
 from tandem_amd.layers import awq, w4_hip
 
 pytestmark = pytest.mark.gpu
@@ -52,18 +53,6 @@ class Case:
 
     def x(self, m: int, seed: int) -> np.ndarray:
         return np.random.default_rng(seed).standard_normal((m, self.k)).astype(np.float16)
-
-
-def check_close(y: torch.Tensor, ref: np.ndarray, atol: float, rtol: float, what) -> None:
-    got = y.float().cpu().numpy().astype(np.float64)
-    assert got.shape == ref.shape, (what, got.shape, ref.shape)
-    err = np.abs(got - ref)
-    bad = err > atol + rtol * np.abs(ref)
-    max_rel = float(err.max() / max(np.abs(ref).max(), 1e-6))
-    denom = np.linalg.norm(got) * np.linalg.norm(ref)
-    cos = float((got * ref).sum() / denom) if denom > 0 else 1.0
-    assert not bad.any(), (what, f"max|err| {err.max():.4g}", f"max_rel {max_rel:.3g}", f"cos {cos:.7f}")
-    assert cos >= 0.9999 or np.abs(ref).max() < 1e-3, (what, cos)
 
 
 # ------------------------------------------------------------------ repack and dequantization
@@ -110,7 +99,7 @@ def test_gemv_every_config(ext):
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
             for cfg in DECODE_CONFIGS:
-                check_close(ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg))
+                check_close(ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg), "gemv")
 
 
 def test_gemv_silu_mul(ext):
@@ -125,7 +114,7 @@ def test_gemv_silu_mul(ext):
             for cfg in DECODE_CONFIGS:
                 y = ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg, 1)
                 assert y.shape == (m, n // 2)
-                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg), "gemv")
 
 
 def test_gemv_mfma_every_config(ext):
@@ -138,7 +127,7 @@ def test_gemv_mfma_every_config(ext):
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
             for cfg in DECODE_CONFIGS:
-                check_close(ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg))
+                check_close(ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, n, m, cfg), "gemvm")
     for k, n in ((128, 32), (1024, 512), (4096, 1024)):
         c = Case(k, n, seed=32, interleave=True)
         for m in range(1, 5):
@@ -148,7 +137,7 @@ def test_gemv_mfma_every_config(ext):
             for cfg in DECODE_CONFIGS:
                 y = ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg, 1)
                 assert y.shape == (m, n // 2)
-                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg))
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg), "gemvm")
 
 
 def _norm_inputs(m: int, k: int, seed: int):
@@ -204,7 +193,7 @@ def test_decode_norm_small_k_against_oracle(ext):
                 for k01, atol, rtol in ((0, 0.05, 0.02), (1, 0.02, 0.01)):
                     y, r_out = ext.w4_decode_norm(gpu(x), gpu(r), gpu(w), 1e-6, c.packed, c.s, c.zz, k01, *cfg, 0)
                     assert (r_out.cpu().numpy().view(np.uint16) == r2.view(np.uint16)).all()
-                    check_close(y, ref, atol, rtol, (k, n, m, cfg, k01))
+                    check_close(y, ref, atol, rtol, (k, n, m, cfg, k01), "norm")
 
 
 def test_mma_every_config(ext):
@@ -216,7 +205,7 @@ def test_mma_every_config(ext):
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
             for cfg in DECODE_CONFIGS:
-                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg))
+                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg), "mma")
 
 
 def _wide_ok(cfg, m) -> bool:
@@ -238,7 +227,7 @@ def test_mma_wide_batches(ext):
                     with pytest.raises(RuntimeError):
                         ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0)
                     continue
-                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg))
+                check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg), "mma")
 
 
 def test_mma_wide_silu_mul(ext):
@@ -252,7 +241,7 @@ def test_mma_wide_silu_mul(ext):
                 if _wide_ok(cfg, m):
                     y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
                     assert y.shape == (m, n // 2)
-                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg))
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg), "mma")
 
 
 def test_mma_silu_mul(ext):
@@ -266,7 +255,7 @@ def test_mma_silu_mul(ext):
             for cfg in DECODE_CONFIGS:
                 y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
                 assert y.shape == (m, n // 2)
-                check_close(y, ref, 0.02, 0.01, (k, n, m, cfg))
+                check_close(y, ref, 0.02, 0.01, (k, n, m, cfg), "mma")
 
 
 def test_mma_split_k_every_config(ext):
@@ -289,7 +278,7 @@ def test_mma_split_k_every_config(ext):
                         continue
                     y = ext.w4_mma_splitk(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, int(interleave))
                     ran += 1
-                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits, interleave))
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits, interleave), "mmak")
     torch.cuda.synchronize()
     assert int(locks.abs().sum()) == 0
     assert ran > 3 * len(DECODE_CONFIGS)
@@ -318,7 +307,7 @@ def test_mma_persistent_matches_mma(ext):
                     y = ext.w4_mma_persist(xg, c.packed, c.s, c.zz, *cfg, per_cu, int(interleave))
                     ran += 1
                     assert torch.equal(y, one), (k, n, m, cfg, per_cu, interleave)
-            check_close(one, ref, 0.02, 0.01, (k, n, m, interleave))
+            check_close(one, ref, 0.02, 0.01, (k, n, m, interleave), "mmap")
     assert ran == (4 * 3 * 3 - 4) * len(DECODE_CONFIGS)
 
 
@@ -342,9 +331,9 @@ def test_mma_split_k_deterministic_and_graph_replay(ext):
         x.copy_(gpu(xn))
         graph.replay()
         torch.cuda.synchronize()
-        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "split-K replay")
+        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "split-K replay", "mmak")
         check_close(ext.w4_mma_splitk(x, c.packed, c.s, c.zz, buf, locks, *cfg, 0), o.linear(xn, c.w_exact),
-                    0.02, 0.01, "split-K eager")
+                    0.02, 0.01, "split-K eager", "mmak")
     assert int(locks.abs().sum()) == 0
 
 
@@ -375,7 +364,7 @@ def test_gemm_every_config(ext):
                             (cfg[4] == 1 and m > 16 * cfg[0] and "> 16 mt" in str(e)), (cfg, splits, str(e))
                         continue
                     ran += 1
-                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits), "gemm")
     torch.cuda.synchronize()
     assert int(locks.abs().sum()) == 0
     assert ran > len(GEMM_CONFIGS) * len(SHAPES)
@@ -401,7 +390,30 @@ def test_gemm_silu_mul(ext):
                             (cfg[4] == 1 and m > 16 * cfg[0] and "> 16 mt" in str(e)), (cfg, splits, str(e))
                         continue
                     assert y.shape == (m, n // 2)
-                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits))
+                    check_close(y, ref, 0.02, 0.01, (k, n, m, cfg, splits), "gemm")
+    torch.cuda.synchronize()
+    assert int(locks.abs().sum()) == 0
+
+
+def test_gemm_lds_partial_bands_and_blocks(ext):
+    """The stages-3 GEMM where several N blocks end in a partial one (N = 784: three 256-row blocks
+    and a 16-row one) and the token bands of 8 blocks end in a partial band (M = 1100 at BM = 128:
+    nine blocks), plain and SwiGLU, unsplit, auto-split and split 3 ways: the band / block remap and
+    the last-tile clamp against the oracle."""
+    buf, locks = w4_hip.workspace(DEV)
+    lds_cfgs = [cfg for cfg in GEMM_CONFIGS if cfg[4] == 3]
+    assert lds_cfgs
+    for act in (0, 1):
+        c = Case(1024, 784, seed=41 + act, interleave=bool(act))
+        for m in (1100, 300):
+            x = c.x(m, seed=4100 + m)
+            ref = o.swiglu_reference(x, c.w_exact) if act else o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in lds_cfgs:
+                for splits in (1, 0, 3):
+                    y = ext.w4_gemm(xg, c.packed, c.s, c.zz, buf, locks, *cfg, splits, act)
+                    assert y.shape == (m, 392 if act else 784)
+                    check_close(y, ref, 0.02, 0.01, (1024, 784, m, cfg, splits), "gemm s3")
     torch.cuda.synchronize()
     assert int(locks.abs().sum()) == 0
 
@@ -435,7 +447,7 @@ def test_gemm_split_k_graph_replay(ext, cfg):
         x.copy_(gpu(xn))
         graph.replay()
         torch.cuda.synchronize()
-        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "replay")
+        check_close(y, o.linear(xn, c.w_exact), 0.02, 0.01, "replay", "gemm")
     assert int(locks.abs().sum()) == 0
 
 
@@ -480,15 +492,16 @@ def test_qwen3_8b_shapes(ext, proj):
     buf, locks = w4_hip.workspace(DEV)
     for m in (1, 4):
         x = c.x(m, seed=m)
-        check_close(ext.w4_gemv(gpu(x), c.packed, c.s, c.zz, 4, 2, 1), o.linear(x, c.w_exact), 0.05, 0.02, (proj, m))
+        check_close(ext.w4_gemv(gpu(x), c.packed, c.s, c.zz, 4, 2, 1), o.linear(x, c.w_exact), 0.05, 0.02, (proj, m),
+                    "gemv")
     for m in (1, 8, 16):
         x = c.x(m, seed=m)
         check_close(ext.w4_mma(gpu(x), c.packed, c.s, c.zz, 4, 2, 1, 0), o.linear(x, c.w_exact), 0.02, 0.01,
-                    (proj, m))
+                    (proj, m), "mma")
     for m, cfg in ((32, (2, 1, 4, 1, 2, 0)), (64, (4, 1, 4, 1, 2, 0)), (256, (8, 2, 4, 1, 2, 0))):
         x = c.x(m, seed=m)
         check_close(ext.w4_gemm(gpu(x), c.packed, c.s, c.zz, buf, locks, *cfg, 0), o.linear(x, c.w_exact), 0.02,
-                    0.01, (proj, m, cfg))
+                    0.01, (proj, m, cfg), "gemm")
 
 
 # --------------------------------------------------------------------------- W4Linear layer
@@ -513,16 +526,16 @@ def test_w4linear_small_and_large_batch():
     rng = np.random.default_rng(20)
     for m in (1, 3, 8, 12, 16, 37, 300):
         x = rng.standard_normal((m, k)).astype(np.float16)
-        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, m)
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, m, "layer")
     for m in (3, 40):  # not 16-byte aligned: dequantize + matmul
         xu = torch.empty(m * k + 1, device=DEV, dtype=torch.float16)[1:].view(m, k)
         xn = rng.standard_normal((m, k)).astype(np.float16)
         xu.copy_(gpu(xn))
-        check_close(layer(xu), o.linear(xn, c.w_exact), 0.05, 0.02, ("unaligned", m))
+        check_close(layer(xu), o.linear(xn, c.w_exact), 0.05, 0.02, ("unaligned", m), "layer")
     for cfg in ((2, 2, 4, 2, 2, 2), (4, 2, 4, 1, 2, 0), ("mma", 8, 1, 1), None):
         layer.gemm_kernels = {(n, k): ((1 << 30, cfg),)}
         x = rng.standard_normal((50, k)).astype(np.float16)
-        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, cfg)
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, cfg, "layer")
     assert layer(torch.empty(0, k, device=DEV, dtype=torch.float16)).shape == (0, n)
 
 
@@ -536,11 +549,11 @@ def test_w4linear_silu_mul():
         x = rng.standard_normal((m, k)).astype(np.float16)
         y = layer(gpu(x))
         assert y.shape == (m, n // 2)
-        check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, m)
+        check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, m, "layer")
     xu = torch.empty(3 * k + 1, device=DEV, dtype=torch.float16)[1:].view(3, k)
     xn = rng.standard_normal((3, k)).astype(np.float16)
     xu.copy_(gpu(xn))
-    check_close(layer(xu), o.swiglu_reference(xn, c.w_exact), 0.03, 0.02, "unaligned")
+    check_close(layer(xu), o.swiglu_reference(xn, c.w_exact), 0.03, 0.02, "unaligned", "layer")
 
 
 def test_w4linear_gemm_switch_off(monkeypatch):
@@ -548,7 +561,7 @@ def test_w4linear_gemm_switch_off(monkeypatch):
     layer, c = _layer(256, 128, seed=22)
     monkeypatch.setattr(awq, "FUSED_GEMM", False)
     x = np.random.default_rng(22).standard_normal((40, 256)).astype(np.float16)
-    check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, "switch off")
+    check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, "switch off", "dense")
 
 
 @pytest.mark.parametrize("proj,silu", [("gate_up", True), ("gate_up", False), ("down", False), ("qkv", False),
@@ -565,10 +578,11 @@ def test_w4linear_qwen3_8b_tables(proj, silu):
     for m in (1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 20, 24, 32, 48, 64, 96, 130):
         x = rng.standard_normal((m, k)).astype(np.float16)
         y = layer(gpu(x))
+        kern = layer.kernel_for(m).split("(")[0]
         if silu:
-            check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, (proj, m))
+            check_close(y, o.swiglu_reference(x, c.w_exact), 0.03, 0.02, (proj, m), kern, f"{proj}+silu")
         else:
-            check_close(y, o.linear(x, c.w_exact), 0.05, 0.02, (proj, m))
+            check_close(y, o.linear(x, c.w_exact), 0.05, 0.02, (proj, m), kern)
 
 
 def test_w4linear_qwen3_0_6b_qkv_table():
@@ -581,4 +595,4 @@ def test_w4linear_qwen3_0_6b_qkv_table():
         if m <= 8:
             assert (4096, 1024, m) in layer.kernels, m
         x = rng.standard_normal((m, 1024)).astype(np.float16)
-        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, ("0.6b qkv", m))
+        check_close(layer(gpu(x)), o.linear(x, c.w_exact), 0.05, 0.02, ("0.6b qkv", m), "layer")

@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from oracle import awq_oracle as o
+from parity import check_close
 from tandem_amd.layers import awq, gemv16, w4_hip
 
 pytestmark = pytest.mark.gpu
@@ -31,18 +32,6 @@ QWEN3_8B = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "d
 
 def gpu(a) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-
-
-def check_close(got: np.ndarray, ref: np.ndarray, atol: float, rtol: float, what) -> None:
-    got = np.asarray(got, dtype=np.float64)
-    assert got.shape == ref.shape, (what, got.shape, ref.shape)
-    err = np.abs(got - ref)
-    max_rel = float(err.max() / max(np.abs(ref).max(), 1e-6))
-    denom = np.linalg.norm(got) * np.linalg.norm(ref)
-    cos = float((got * ref).sum() / denom) if denom > 0 else 1.0
-    assert not (err > atol + rtol * np.abs(ref)).any(), (what, f"max|err| {err.max():.4g}", f"max_rel {max_rel:.3g}",
-                                                          f"cos {cos:.7f}")
-    assert cos >= 0.9999, (what, cos)
 
 
 def awq_layer(k: int, n: int, seed: int, silu: bool = False):
@@ -83,10 +72,12 @@ def test_qwen3_1_7b_tables(proj, silu):
         assert key in layer.kernels or (n, k, m) in layer.kernels, key
         x = rng.standard_normal((m, k)).astype(np.float16)
         y = layer(gpu(x)).float().cpu().numpy()
+        kern = layer.kernel_for(m).split("(")[0]
         if silu:
-            check_close(y, o.swiglu_reference(x, w_exact), 0.03, 0.02, (proj, m, layer.decode_entry(m)))
+            check_close(y, o.swiglu_reference(x, w_exact), 0.03, 0.02, (proj, m, layer.decode_entry(m)), kern,
+                        f"1.7b {proj}+silu")
         else:
-            check_close(y, o.linear(x, w_exact), 0.05, 0.02, (proj, m, layer.decode_entry(m)))
+            check_close(y, o.linear(x, w_exact), 0.05, 0.02, (proj, m, layer.decode_entry(m)), kern, f"1.7b {proj}")
 
 
 @pytest.mark.parametrize("proj,silu", [("qkv", False), ("o", False), ("gate_up", True), ("down", False)])
@@ -115,7 +106,9 @@ def test_qwen3_8b_prefill_sizes(proj, silu):
         for what, cfg, y in runs:
             assert y.shape == (m, n_out)
             got = y[:, torch.from_numpy(feats).to(DEV)].float().cpu().numpy()
-            check_close(got, ref, 0.03 if silu else 0.05, 0.02, (proj, m, what, cfg))
+            kern = "dequant+matmul" if cfg is None else ("mma" if cfg[0] == "mma" else f"gemm s{cfg[4]}")
+            check_close(got, ref, 0.03 if silu else 0.05, 0.02, (proj, m, what, cfg), kern,
+                        f"{proj}{'+silu' if silu else ''}")
         del xg, runs
     torch.cuda.synchronize()
     assert int(locks.abs().sum()) == 0
@@ -196,8 +189,9 @@ def test_full_stack_graph_equals_eager(stack, m):
         feats = np.sort(rng.choice(n_out, size=min(n_out, 1024), replace=False))
         ref = sampled_reference(x_np[k], host0[proj], feats, n, silu)
         got = eager[i][:, torch.from_numpy(feats).to(DEV)].float().cpu().numpy()
-        check_close(got, ref, 0.03 if silu else 0.05, 0.02, ("layer 0", proj, m))
+        check_close(got, ref, 0.03 if silu else 0.05, 0.02, ("layer 0", proj, m),
+                    layers[0][proj].kernel_for(m).split("(")[0], f"stack {proj}", m)
     rows = np.sort(rng.choice(HEAD[0], size=2048, replace=False))
     w_rows = head[torch.from_numpy(rows).to(DEV)].cpu().numpy()
     check_close(eager[-1][:, torch.from_numpy(rows).to(DEV)].float().cpu().numpy(), o.linear(x_np[4096], w_rows),
-                0.02, 0.01, ("lm_head", m))
+                0.02, 0.01, ("lm_head", m), "gemv16", "lm_head", m)

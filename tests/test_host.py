@@ -220,6 +220,38 @@ def test_pick_gemm_ladder():
     assert awq.pick_gemm(((64, "x"),), 100) == "x"  # past the last m_max: the last entry
 
 
+def test_huge_batches_take_the_dense_path(monkeypatch):
+    """M x K >= 2^31 is beyond the fused GEMM's 32-bit offsets (the reference's w4_gemm refuses it,
+    csrc/w4_gemv.cu:661): forward's GEMM predicate sends it to dequantize + matmul, whatever the
+    ladder says, and kernel_for reports the same routing."""
+    import types
+
+    layer = awq.W4Linear(4096, 4096, 128)
+    layer.awq_layout = False
+    layer.gemm_kernels = {(4096, 4096): ((1 << 30, (8, 4, 4, 1, 3, 0)),)}
+    assert layer.kernel_for(524287).startswith("gemm(")
+    assert layer.kernel_for(524288) == "dequant+matmul"  # 524288 x 4096 = 2^31
+    monkeypatch.setattr(awq, "_aligned", lambda x: True)
+    fake = lambda m: types.SimpleNamespace(is_cuda=True, shape=(m, 4096))  # noqa: E731
+    assert awq._gemm_ok(fake(524287)) and not awq._gemm_ok(fake(524288)) and not awq._gemm_ok(fake(16))
+
+
+def test_kernel_for_follows_the_tables():
+    """kernel_for names the entry forward dispatches: the decode table up to M = 16 (gemv / gemvm
+    only up to M = 4, else the default matrix-core kernel), the ladder above, None as dequant + matmul."""
+    layer = awq.W4Linear(256, 64, 128)
+    layer.awq_layout = False
+    layer.kernels = {(64, 256, 1): ("gemv", 4, 2, 1), (64, 256, 6): ("gemv", 4, 2, 1),
+                     (64, 256, 8): ("mmak", 8, 1, 2, 2)}
+    layer.gemm_kernels = {(64, 256): ((32, ("mma", 8, 1, 1)), (64, (2, 1, 4, 2, 2, 4)), (1 << 30, None))}
+    assert layer.kernel_for(1) == "gemv(4, 2, 1)"
+    assert layer.kernel_for(6) == f"{awq.DEFAULT_KERNEL[0]}{tuple(awq.DEFAULT_KERNEL[1:])}"
+    assert layer.kernel_for(8) == "mmak(8, 1, 2, 2)"
+    assert layer.kernel_for(20) == "mma(8, 1, 1)"
+    assert layer.kernel_for(40) == "gemm(2, 1, 4, 2, 2, 4)"
+    assert layer.kernel_for(100) == "dequant+matmul"
+
+
 def test_tables_are_well_formed():
     assert awq.DEFAULT_KERNEL[0] in ("gemv", "mma") and len(awq.DEFAULT_KERNEL) == 4
     decode = set(w4_hip.decode_configs())

@@ -185,6 +185,20 @@ def test_swiglu_reference_rounds_weights_once():
     assert np.allclose(o.swiglu_reference(x, w), want, rtol=0, atol=0)
 
 
+def test_random_awq_recipe():
+    """The reference tests' input recipe (tests/test_awq.py:32-38): q and z uniform over all of 0..15,
+    scales fp16 in [0.001, 0.021), AutoAWQ-packed q and z, the group dimension K / 128."""
+    qw, qz, s, q, z = o.random_awq(1024, 64, seed=3)
+    assert qw.shape == (1024, 8) and qz.shape == (8, 8) and s.shape == (8, 64) and s.dtype == np.float16
+    assert q.shape == (1024, 64) and z.shape == (8, 64)
+    assert set(np.unique(q)) == set(range(16)) and set(np.unique(z)) == set(range(16))
+    assert (o.unpack_awq(qw) == q).all() and (o.unpack_awq(qz) == z).all()
+    sf = s.astype(np.float64)
+    assert sf.min() >= 0.001 - 1e-6 and sf.max() < 0.021 + 1e-5 and sf.std() > 0.005
+    qw2, _, s2, _, _ = o.random_awq(1024, 64, seed=3)
+    assert (qw2 == qw).all() and (s2.view(np.uint16) == s.view(np.uint16)).all()  # seeded
+
+
 # ---------------------------------------------------------------------------- golden fixtures
 def test_golden_fixtures():
     """The committed fixtures (tests/golden/make_golden.py) still come out of the oracle."""

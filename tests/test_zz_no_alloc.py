@@ -25,9 +25,8 @@ def test_noalloc_matches_workspace_entry_point():
     ext = w4_hip.load()
     buf, locks = w4_hip.workspace("cuda")
     rng = np.random.default_rng(77)
-    # (K, N, act, M of the first call, M of the second, config with splits). A splits = 0 case must pick
-    # the same split count from either workspace size (the stages-3 launcher sizes it by the workspace),
-    # so the stages-3 case names its split.
+    # (K, N, act, M of the first call, M of the second, config with splits). splits = 0 chooses its split
+    # within a fixed budget, never from the workspace it is given, so both entry points run the same one.
     cases = [(4096, 6144, 0, 64, 33, (2, 1, 4, 2, 2, 4)),     # every tile split 4 ways
              (12288, 4096, 0, 64, 20, (2, 1, 4, 1, 2, 0)),    # the last partial wave split
              (4096, 2048, 1, 130, 17, (4, 2, 4, 1, 2, 2)),    # SwiGLU epilogue, split 2
@@ -35,6 +34,7 @@ def test_noalloc_matches_workspace_entry_point():
              (12288, 4096, 0, 32, 20, (2, 4, 1, 4, 1, 4)),    # x from L2 (stages 1), split 4
              (4096, 2048, 1, 16, 9, (1, 2, 2, 8, 1, 0)),      # stages 1 at decode M, SwiGLU, auto split
              (4096, 2048, 0, 300, 130, (8, 4, 4, 1, 3, 2)),   # both tiles through LDS (stages 3), split 2
+             (4096, 2048, 0, 300, 130, (8, 4, 4, 1, 3, 0)),   # stages 3, automatic split (10 ways at M 300)
              (1024, 512, 0, 300, 50, (8, 2, 4, 1, 2, 1))]     # no split
     for k, n, act, m1, m2, cfg in cases:
         packed, s, z, w = _weights(k, n, seed=k + n + act, interleave=bool(act))
@@ -62,6 +62,21 @@ def test_noalloc_refuses_a_split_beyond_its_scratch():
     y = ext.w4_gemm_noalloc(x[:32].contiguous(), packed, s, z, 2, 1, 4, 2, 2, 2, 0)
     buf, locks = w4_hip.workspace("cuda")
     assert torch.equal(y, ext.w4_gemm(x[:32].contiguous(), packed, s, z, buf, locks, 2, 1, 4, 2, 2, 2, 0))
+
+
+def test_automatic_split_does_not_depend_on_the_workspace():
+    """splits = 0 with a workspace smaller than the split it picks is refused (TW4_ESPACE), not run
+    with fewer splits and other bits; with the full workspace it runs and equals the no-alloc call."""
+    ext = w4_hip.load()
+    packed, s, z, _ = _weights(4096, 2048, seed=21)
+    x = torch.randn(300, 4096, device="cuda", dtype=torch.float16)
+    buf, locks = w4_hip.workspace("cuda")
+    cfg = (8, 4, 4, 1, 3, 0)  # 24 tiles of 128 x 256, 10 splits: 7.9 M partials
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        ext.w4_gemm(x, packed, s, z, buf[:1 << 21], locks, *cfg, 0)
+    want = ext.w4_gemm(x, packed, s, z, buf, locks, *cfg, 0)
+    assert torch.equal(ext.w4_gemm_noalloc(x, packed, s, z, *cfg, 0), want)
+    assert int(locks.abs().sum()) == 0
 
 
 def test_noalloc_graph_replay():
