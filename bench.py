@@ -658,7 +658,7 @@ def tune_main(argv=None) -> int:
                     nw = (torch.rand(k, device=dev) + 0.5).half()
                     attempt(res, ("gemvn", *cfg),
                             [lambda w=w, c=cfg: ext.w4_decode_norm(x, r, nw, 1e-6, *w, 0, *c, act) for w in ws])
-                if "gemvm" in kinds and m <= 4:
+                if "gemvm" in kinds and m <= 16:
                     attempt(res, ("gemvm", *cfg), [lambda w=w, c=cfg: ext.w4_gemv_mfma(x, *w, *c, act) for w in ws])
                 if "mma" in kinds and m <= 64:
                     attempt(res, ("mma", *cfg), [lambda w=w, c=cfg: ext.w4_mma(x, *w, *c, act) for w in ws])

@@ -96,11 +96,13 @@ int tw4_gemv_act(const uint16_t* x, const int32_t* packed, const uint16_t* scale
                  const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                  int warps_k, int unroll, int ntile, int act, void* stream);
 
-/* The GEMV's arithmetic on the matrix cores, 1 <= M <= 4: raw magic halves (1024 + q) times x' on
- * v_mfma_f32_16x16x32_f16, the bias and the zero point in the accumulator's start value, the scale
- * per group; exact (q - z) weights like tw4_gemv (so the GEMV's tolerance). Same configs, act and
- * limits as tw4_gemv_act (scales and zeros 8-byte aligned). No reference counterpart: an alternative
- * kernel for the (N, K, M) table entries of w4_gemv (python/tandem/layers/awq.py:136-160). */
+/* The GEMV's arithmetic on the matrix cores, 1 <= M <= 16 (one 16-column B tile): raw magic halves
+ * (1024 + q) times x' on v_mfma_f32_16x16x32_f16, the bias and the zero point in the accumulator's
+ * start value, the scale per group; exact (q - z) weights like tw4_gemv (so the GEMV's tolerance).
+ * Same configs and act as tw4_gemv_act; x' of M rows and its per-group sums must fit in LDS
+ * (TW4_EINVAL otherwise: K = 4096 takes M <= 16, K = 12288 M <= 4); scales and zeros 8-byte aligned.
+ * No reference counterpart: an alternative kernel for the (N, K, M) decode-table entries of w4_gemv
+ * and w4_mma (python/tandem/layers/awq.py:136-160). */
 int tw4_gemv_mfma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
                   const uint16_t* zeros, uint16_t* y, int M, int N, int K,
                   int warps_k, int unroll, int ntile, int act, void* stream);

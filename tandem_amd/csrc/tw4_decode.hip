@@ -7,7 +7,7 @@
 namespace tw4 {
 
 // ----------------------------------------------------------------------------------- gemvm
-// The GEMV's arithmetic on the matrix cores, M <= 4. A = the raw magic halves of a word (1024 + q,
+// The GEMV's arithmetic on the matrix cores, M <= 16. A = the raw magic halves of a word (1024 + q,
 // or 1024 + 16 q for the high nibbles: no zero point, no scale), B = x' (pairs 2, 3, 6, 7 divided
 // by 16), so one v_mfma_f32_16x16x32_f16 does the 32 products that take 16 v_dot2 per batch row
 // on the vector ALUs. The bias and the zero point come off in the accumulator's start value,
@@ -44,8 +44,7 @@ __device__ __forceinline__ void load_chunk_m(WeightSetM<U, NT>& ws, const TileSt
 __host__ __device__ __forceinline__ int gemvm_gcorr_u4(int M, int K) { return (M * (K >> 7) * 8 + 15) / 16; }
 
 // After staging: the group sums (-1024 A_g, B_g) of the wavefront's groups from the slice sums.
-template <int M>
-__device__ __forceinline__ void group_corr(const float2* corr, float2* gcorr, int G, int gb, int ge, int lane) {
+__device__ __forceinline__ void group_corr(const float2* corr, float2* gcorr, int G, int gb, int ge, int M, int lane) {
     const int n = (ge - gb) * M;
     for (int j = lane; j < n; j += 64) {
         const int m = j / (ge - gb), g = gb + (j - m * (ge - gb));
@@ -57,7 +56,7 @@ __device__ __forceinline__ void group_corr(const float2* corr, float2* gcorr, in
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <bool PF, int M, int U, int NT>
+template <bool PF, int U, int NT>
 __device__ __forceinline__ void gemvm_chunk(const WeightSetM<U, NT>& cur, WeightSetM<U, NT>& nxt,
                                             const TileStreams<NT>& ts, const uint16_t* s16, const uint16_t* z16,
                                             const u4* lx, const float2* gcorr, const DecodeLds& l, f4 (&acc)[NT],
@@ -99,10 +98,12 @@ __device__ __forceinline__ void gemvm_chunk(const WeightSetM<U, NT>& cur, Weight
     }
 }
 
-template <int M, int WK, int U, int NT>
+// M (1 .. 16, the columns of one B tile) is a kernel argument; ONE: M == 1, where the x staging needs
+// no division by the row length.
+template <bool ONE, int WK, int U, int NT>
 __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                        const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                       h1* __restrict__ y, int N, int K, int act) {
+                                                       h1* __restrict__ y, int M, int N, int K, int act) {
     extern __shared__ u4 smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
@@ -125,12 +126,12 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
     WeightSetM<U, NT> a, b;
     {  // no branch around the first loads (see gemv_kernel); an empty slice reads valid addresses
         u4 xfirst[kXB];
-        load_x_batch<M == 1>(xfirst, xg, kx, xsl, lane);
+        load_x_batch<ONE>(xfirst, xg, kx, xsl, lane);
         __builtin_amdgcn_sched_barrier(0);
         load_chunk_m<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0), kb);
         __builtin_amdgcn_sched_barrier(0);
-        stage_x<true, M == 1>(smem, l, corr, xg, kx, xsl, xfirst, lane);
-        group_corr<M>(corr, gcorr, G, gb, ge, lane);
+        stage_x<true, ONE>(smem, l, corr, xg, kx, xsl, xfirst, lane);
+        group_corr(corr, gcorr, G, gb, ge, M, lane);
     }
 
     f4 acc[NT];
@@ -138,14 +139,14 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
     for (int t = 0; t < NT; ++t) acc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
     for (; i + 2 < nch; i += 2) {
-        gemvm_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
-        gemvm_chunk<true, M, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
+        gemvm_chunk<true, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+        gemvm_chunk<true, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
     }
     if (i + 2 == nch) {
-        gemvm_chunk<true, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
-        gemvm_chunk<false, M, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
+        gemvm_chunk<true, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+        gemvm_chunk<false, U, NT>(b, a, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * (i + 1), ge, G, kb, magic);
     } else if (i + 1 == nch) {
-        gemvm_chunk<false, M, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
+        gemvm_chunk<false, U, NT>(a, b, ts, s16, z16, smem, gcorr, l, acc, xrow, gb + U * i, ge, G, kb, magic);
     }
     if (WK > 1) {
         f4* red = reinterpret_cast<f4*>(smem + l.red);  // [WK - 1][NT][64]
@@ -453,10 +454,8 @@ int decode_prepare(int dev) {
 #define TW4_ATTR(WK, U, T)                                                   \
     TW4_ATTR_GEMV(WK, U, T, false)                                           \
     TW4_ATTR_GEMV(WK, U, T, true)                                            \
-    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<1, WK, U, T>);             \
-    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<2, WK, U, T>);             \
-    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<3, WK, U, T>);             \
-    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<4, WK, U, T>);             \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<true, WK, U, T>);          \
+    if (rc == TW4_OK) rc = allow_lds(gemvm_kernel<false, WK, U, T>);         \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds>);         \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLds, true>);   \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 1, kXLdsWide>);     \
@@ -481,9 +480,8 @@ int ensure_prepared() {
     return decode_prepare(dev);
 }
 
-template <int M>
-int gemvm_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int N, int K, int wk, int un, int nt,
-                   int act, hipStream_t st) {
+int gemvm_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, int M, int N, int K, int wk, int un,
+                   int nt, int act, hipStream_t st) {
     const int tiles = (N + 15) >> 4;
 #define TW4_GEMVM_CASE(WK, U, T)                                                                             \
     if (wk == WK && un == U && nt == T) {                                                                    \
@@ -491,7 +489,10 @@ int gemvm_dispatch(const h1* x, const u4* w, const h1* s, const h1* z, h1* y, in
                                     decode_lds(true, M, K, gemv_corr_u4(M, K) + gemvm_gcorr_u4(M, K), (WK - 1) * T * 64).total); \
         TW4_REQUIRE(lds <= static_cast<size_t>(kMaxLds), TW4_EINVAL,                                        \
                     "gemv_mfma: x [%d, %d] does not fit in LDS (use mma)", M, K);                            \
-        gemvm_kernel<M, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, N, K, act);       \
+        if (M == 1)                                                                                          \
+            gemvm_kernel<true, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, M, N, K, act); \
+        else                                                                                                 \
+            gemvm_kernel<false, WK, U, T><<<(tiles + T - 1) / T, WK * 64, lds, st>>>(x, w, s, z, y, M, N, K, act); \
         TW4_LAUNCH_CHECK("gemv_mfma: launch");                                                               \
         return TW4_OK;                                                                                       \
     }
@@ -549,7 +550,7 @@ extern "C" int tw4_gemv_mfma(const uint16_t* x, const int32_t* packed, const uin
                              void* stream) {
     int rc = check_operands("gemv_mfma", x, packed, scales, zeros, y, M, N, K);
     if (rc) return rc;
-    TW4_REQUIRE(M >= 1 && M <= 4, TW4_EINVAL, "gemv_mfma: 1 <= M <= 4 (M = %d; larger M: mma)", M);
+    TW4_REQUIRE(M >= 1 && M <= 16, TW4_EINVAL, "gemv_mfma: 1 <= M <= 16 (M = %d; larger M: mma)", M);
     TW4_REQUIRE(reinterpret_cast<uintptr_t>(scales) % 8 == 0 && reinterpret_cast<uintptr_t>(zeros) % 8 == 0,
                 TW4_EINVAL, "gemv_mfma: scales and zeros must be 8-byte aligned");
     TW4_REQUIRE(K <= 65536, TW4_EINVAL, "gemv_mfma: K <= 65536 (K = %d; larger K: mma)", K);
@@ -563,12 +564,7 @@ extern "C" int tw4_gemv_mfma(const uint16_t* x, const int32_t* packed, const uin
     auto zp = reinterpret_cast<const h1*>(zeros);
     auto yp = reinterpret_cast<h1*>(y);
     auto st = static_cast<hipStream_t>(stream);
-    switch (M) {
-        case 1: return gemvm_dispatch<1>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        case 2: return gemvm_dispatch<2>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        case 3: return gemvm_dispatch<3>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-        default: return gemvm_dispatch<4>(xp, wp, sp, zp, yp, N, K, warps_k, unroll, ntile, act, st);
-    }
+    return gemvm_dispatch(xp, wp, sp, zp, yp, M, N, K, warps_k, unroll, ntile, act, st);
 }
 
 extern "C" int tw4_gemv(const uint16_t* x, const int32_t* packed, const uint16_t* scales, const uint16_t* zeros,

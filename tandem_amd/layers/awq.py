@@ -143,7 +143,7 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, 
 #   ("gemv", warps_k, unroll, ntile)   vector ALUs, M <= 4 (with the SwiGLU epilogue too: the
 #                                      reference's SwiGLU gate_up always takes "mma")
 #   ("gemvm", warps_k, unroll, ntile)  the GEMV's arithmetic (exact q - z, scale per group) on the
-#                                      matrix cores, M <= 4
+#                                      matrix cores, M <= 16 (x' in LDS: K = 4096 up to M = 16)
 #   ("mma", warps_k, unroll, ntile)    matrix cores, M <= 64
 #   ("mmak", warps_k, unroll, ntile, splits)   the same with K split over `splits` workgroups per
 #                                      row-tile group (x in LDS over 1 / splits of K; the last arriver
@@ -299,7 +299,7 @@ class W4Linear(nn.Module):
             return "empty"
         if m <= 16:
             kind, *cfg = self.decode_entry(m)
-            if kind not in ("gemm", "mmak", "mmap", "mma") and not (kind in ("gemv", "gemvm") and m <= 4):
+            if kind not in ("gemm", "mmak", "mmap", "mma", "gemvm") and not (kind == "gemv" and m <= 4):
                 kind, *cfg = DEFAULT_KERNEL
             return f"{kind}{tuple(cfg)}"
         key = (self.out_features, self.in_features) + (("silu",) if self.silu_mul else ())
@@ -372,7 +372,7 @@ class W4Linear(nn.Module):
                     return self._gemm(ext, x, cfg)
                 if kind == "gemv" and m <= 4:  # with the SwiGLU epilogue too (tw4_gemv_act)
                     return ext.w4_gemv(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
-                if kind == "gemvm" and m <= 4:  # the GEMV's arithmetic on the matrix cores
+                if kind == "gemvm":  # the GEMV's arithmetic on the matrix cores (M <= 16)
                     return ext.w4_gemv_mfma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
                 if kind == "mmak":  # the matrix-core decode kernel with K split over workgroups
                     buf, locks = w4_hip.workspace(x.device)
@@ -380,7 +380,7 @@ class W4Linear(nn.Module):
                                              int(self.silu_mul))
                 if kind == "mmap":  # the matrix-core decode kernel, persistent workgroups
                     return ext.w4_mma_persist(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
-                if kind != "mma":  # gemv / gemvm past M = 4
+                if kind != "mma":  # gemv past M = 4
                     _, *cfg = DEFAULT_KERNEL
                 return ext.w4_mma(x, self.packed, self.scales, self.zeros, *cfg, int(self.silu_mul))
         elif _gemm_ok(x):  # M > 16: the GEMM, unless the table prefers dequantize + torch.matmul

@@ -174,10 +174,11 @@ class W4Extension:
         return y
 
     def w4_gemv_mfma(self, x, w, s, z, warps_k: int, unroll: int, ntile: int, act: int = 0) -> torch.Tensor:
-        """The GEMV's arithmetic on the matrix cores (tw4_gemv_mfma; no reference counterpart), M <= 4."""
+        """The GEMV's arithmetic on the matrix cores (tw4_gemv_mfma; no reference counterpart), M <= 16
+        (x' of M rows must fit in LDS: K = 4096 takes any M <= 16, K = 12288 M <= 4)."""
         m, n, k = check_operands("w4_gemv_mfma", x, w, s, z)
-        if not 1 <= m <= 4:
-            raise RuntimeError("w4_gemv_mfma: M <= 4 (larger M: w4_mma)")
+        if not 1 <= m <= 16:
+            raise RuntimeError("w4_gemv_mfma: M <= 16 (larger M: w4_mma)")
         if act not in (0, 1) or (act and n % 16):
             raise RuntimeError("w4_gemv_mfma: act 0, or 1 (SwiGLU) with N % 16 == 0")
         y = torch.empty((m, n // 2 if act else n), dtype=torch.float16, device=x.device)

@@ -140,6 +140,33 @@ def test_gemv_mfma_every_config(ext):
                 check_close(y, ref, 0.05, 0.02, (k, n, m, cfg), "gemvm")
 
 
+def test_gemv_mfma_full_batch_tile(ext):
+    """tw4_gemv_mfma at M = 5 .. 16 (the rest of its 16-column B tile), every compiled config, plain
+    and SwiGLU, including a partial row tile and the largest M whose x' fits in LDS at K = 4096; an
+    M whose x' does not fit is refused on the host."""
+    ran = 0
+    for k, n, act in ((1024, 1000, 0), (4096, 1024, 0), (4096, 512, 1)):
+        c = Case(k, n, seed=33 + act, interleave=bool(act))
+        for m in (5, 8, 13, 16):
+            x = c.x(m, seed=1300 + m)
+            ref = o.swiglu_reference(x, c.w_exact) if act else o.linear(x, c.w_exact)
+            xg = gpu(x)
+            for cfg in DECODE_CONFIGS:
+                try:
+                    y = ext.w4_gemv_mfma(xg, c.packed, c.s, c.zz, *cfg, act)
+                except RuntimeError as e:  # x' plus this config's reduction buffer past 160 KB of LDS
+                    assert m * (2 * k + 16) + (cfg[0] - 1) * cfg[2] * 1024 > 128 * 1024 and \
+                        "does not fit in LDS" in str(e), (k, n, m, cfg, str(e))
+                    continue
+                ran += 1
+                assert y.shape == (m, n // 2 if act else n)
+                check_close(y, ref, 0.05, 0.02, (k, n, m, cfg), "gemvm")
+    assert ran >= 3 * 4 * len(DECODE_CONFIGS) * 3 // 4
+    c = Case(12288, 64, seed=35)
+    with pytest.raises(RuntimeError, match="does not fit in LDS"):
+        ext.w4_gemv_mfma(gpu(c.x(8, seed=1)), c.packed, c.s, c.zz, 4, 2, 1, 0)
+
+
 def _norm_inputs(m: int, k: int, seed: int):
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((m, k)) * 2).astype(np.float16)

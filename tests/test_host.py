@@ -271,9 +271,10 @@ def test_tables_are_well_formed():
             elif cfg[0] == "mmap":  # a compiled decode config, 1 .. 8 workgroups per CU, x in LDS
                 assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 1 <= cfg[4] <= 8
                 assert m * (2 * k + 16) <= 136 * 1024  # past 80 KB only for grids of at most one per CU
-            else:  # a compiled decode config; gemv / gemvm only where they run (M <= 4)
+            else:  # a compiled decode config; gemv only where it runs (M <= 4), gemvm where x' fits LDS
                 assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
-                assert cfg[0] == "mma" or m <= 4
+                assert cfg[0] != "gemv" or m <= 4
+                assert cfg[0] != "gemvm" or m * (2 * k + 16) + m * (k // 128) * 36 <= 160 * 1024
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
         m_maxes = [m for m, _ in ladder]
         assert m_maxes == sorted(m_maxes)
