@@ -104,9 +104,9 @@ def summary(by_test: bool = True) -> list[str]:
             lines.append(f"{t[:40]:40s} {n:6d} {mr:9.2e} {ma:9.2e} {cs:10.7f}  {at:g}/{rt:g}  "
                          f"{'/'.join(sorted(fams))[:24]} M {ms_s}")
         return lines
-    lines.append(f"{'test':36s} {'family':8s} {'shape':12s} {'M':>5s} {'checks':>6s} {'max_rel':>9s} {'max|err|':>9s} "
+    lines.append(f"{'test':44s} {'family':8s} {'shape':12s} {'M':>5s} {'checks':>6s} {'max_rel':>9s} {'max|err|':>9s} "
                  f"{'min cos':>10s}")
     for r in RECORDS.values():
-        lines.append(f"{r.test[:36]:36s} {r.family[:8]:8s} {r.shape[:12]:12s} {r.m[:5]:>5s} {r.count:6d} "
+        lines.append(f"{r.test[:44]:44s} {r.family[:8]:8s} {r.shape[:12]:12s} {r.m[:5]:>5s} {r.count:6d} "
                      f"{r.max_rel:9.2e} {r.max_abs:9.2e} {r.cos:10.7f}")
     return lines
