@@ -64,9 +64,13 @@ __device__ __forceinline__ void scale_zero(uint32_t p, uint32_t& s, uint32_t& z)
 // Workgroups are dealt to the 8 XCDs round robin (workgroup b runs on XCD b mod 8). Within each full
 // group of 8 workgroups the tile index is rotated by b / 8, so the tiles one XCD streams do not all
 // share the same low address bits: measured on MI355X, the XCDs then finish closer together (the
-// M = 1 GEMV on gate_up 10.3 vs 10.4-10.6 us). A permutation of 0 .. gridDim.x - 1.
-__device__ __forceinline__ int xcd_rotated_block() {
-    const int b = blockIdx.x, full = gridDim.x & ~7;
+// M = 1 GEMV on gate_up 10.3 vs 10.4-10.6 us). A permutation of 0 .. nblocks - 1.
+// nblocks is the launch's gridDim.x. The kernels that know it from their explicit arguments pass it
+// computed from them: gridDim.x is a hidden kernel argument placed after the explicit ones, past the
+// argument dwords preloaded into SGPRs, so reading it costs every wavefront a scalar load and a wait
+// before its first weight load (the M = 1 GEMV on gate_up measured 10.2 -> 9.9 us without it).
+__device__ __forceinline__ int xcd_rotated_block(int nblocks) {
+    const int b = blockIdx.x, full = nblocks & ~7;
     return b < full ? (b & ~7) | (((b & 7) + (b >> 3)) & 7) : b;
 }
 
@@ -465,7 +469,7 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int tile0 = xcd_rotated_block() * NT;
+    const int tile0 = xcd_rotated_block((tiles + NT - 1) / NT) * NT;  // the launch's grid
     const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K), gemv_red_u4(M, WK, NT), NORM);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);

@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(WK * 64) gemvm_kernel(const h1* __restrict__ x
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int tile0 = xcd_rotated_block() * NT;
+    const int tile0 = xcd_rotated_block((tiles + NT - 1) / NT) * NT;  // the launch's grid
     const DecodeLds l = decode_lds(true, M, K, gemv_corr_u4(M, K) + gemvm_gcorr_u4(M, K), (WK - 1) * NT * 64);
     const uint32_t magic = magic_reg();
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
@@ -256,14 +256,18 @@ __device__ __forceinline__ void mma_chunk(const WeightSet<U, NT>& cur, WeightSet
 // splits > 1: workgroup (tile group tg, split s) covers quant groups [s G / splits, (s + 1) G / splits)
 // only, with x in LDS over that range alone, and the splits partial sums of a tile group are added by
 // the last arriver (finish_unit: ws / locks, the GEMM's counter protocol).
-// PERSIST: a grid smaller than the tile groups; workgroup u takes tile groups u, u + gridDim.x, ...
+// PERSIST: a grid smaller than the tile groups; workgroup u takes tile groups u, u + nunits, ...
 // with x staged once, each wavefront prefetching the next tile group's first chunk during its last
 // one. Two workgroup barriers per tile group guard the reduction buffer.
+// The arguments the prologue needs (x, the weights, M, N, K, nsplit and nunits = gridDim.x) come first:
+// they fill the 13 argument dwords preloaded into SGPRs, so no wavefront waits on a scalar load before
+// its first weight load; y, act, the norm inputs and the split-K buffers are read later.
 template <int WK, int U, int NT, int MT, int XM, bool NORM = false, bool SPLIT = false, bool PERSIST = false>
 __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                      const h1* __restrict__ scales, const h1* __restrict__ zeros,
-                                                     h1* __restrict__ y, int M, int N, int K, int act, NormIn nin,
-                                                     float* __restrict__ ws, int* __restrict__ locks, int nsplit) {
+                                                     int M, int N, int K, int nsplit, int nunits,
+                                                     h1* __restrict__ y, int act, NormIn nin,
+                                                     float* __restrict__ ws, int* __restrict__ locks) {
     constexpr bool XLDS = XM != kXGlobal;
     constexpr int XB = XM == kXLdsWide ? 8 : 2;
     static_assert(!XLDS || MT == 1, "x in LDS: one batch tile");
@@ -278,7 +282,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
     const int G = K >> 7, tiles = (N + 15) >> 4;
-    const int unit = xcd_rotated_block(), split = unit % splits;
+    const int unit = xcd_rotated_block(nunits), split = unit % splits;
     int tg = unit / splits;
     int tile0 = tg * NT;
     const int glo = split * G / splits, R = (split + 1) * G / splits - glo;  // this workgroup's quant groups
@@ -322,7 +326,7 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
 
     const int ngroups = (tiles + NT - 1) / NT;
     for (int pass = 0;; ++pass) {  // one pass per tile group (PERSIST: several)
-    const int tg_next = tg + static_cast<int>(gridDim.x);
+    const int tg_next = tg + nunits;
     const bool more = PERSIST && tg_next < ngroups;  // uniform across the workgroup
     // The streams the pass's last chunk prefetches from. Last pass: weight blocks of an empty buffer
     // range (out-of-range buffer loads return zeros without a memory access) and the group
@@ -612,56 +616,48 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
                     "mma: split-K workspace too small for %lld tile groups x %d splits", static_cast<long long>(groups),
                     splits);
     }
-#define TW4_MMA_CASE(WK, U, T)                                                                                 \
-    if (warps_k == WK && unroll == U && ntile == T) {                                                          \
-        const int red_u4 = (WK - 1) * T * mt * 64;                                                             \
-        const bool xlds = xlds_small || (mt == 1 && few && x_bytes <= static_cast<size_t>(kXLdsBig) &&         \
+// mma_kernel's arguments in its order; the grid (nunits) is the number of units launched.
+#define TW4_MMA_ARGS(NIN) xp, wp, sp, zp, M, N, K, splits, static_cast<int>(grid), yp, act, NIN, ws, locks
+#define TW4_MMA_CASE(WK, U, T)                                                                                            \
+    if (warps_k == WK && unroll == U && ntile == T) {                                                                     \
+        const int red_u4 = (WK - 1) * T * mt * 64;                                                                        \
+        const bool xlds = xlds_small || (mt == 1 && few && x_bytes <= static_cast<size_t>(kXLdsBig) &&                    \
                                          16 * (static_cast<size_t>(decode_lds(true, M, 128 * R, 0, red_u4).total) + 1) <= \
-                                             static_cast<size_t>(kMaxLds));                                    \
-        const size_t lds = 16 * (static_cast<size_t>(                                                          \
-                                     decode_lds(xlds, M, 128 * R, 0, red_u4, nin != nullptr).total) +          \
-                                 1); /* + the split-K flag */                                                  \
-        const unsigned grid = static_cast<unsigned>(units);                                                   \
-        TW4_REQUIRE(per_cu == 0 || xlds, TW4_ECONFIG, "mma: the persistent form stages x in LDS (M = %d, K = %d)", \
-                    M, K);                                                                                     \
-        if (per_cu > 0 && wide)                                                                                \
-            mma_kernel<WK, U, T, 1, kXLdsWide, false, false, true><<<grid, WK * 64, lds, st>>>(                \
-                xp, wp, sp, zp, yp, M, N, K, act, none, ws, locks, splits);                                    \
-        else if (per_cu > 0)                                                                                   \
-            mma_kernel<WK, U, T, 1, kXLds, false, false, true><<<grid, WK * 64, lds, st>>>(                    \
-                xp, wp, sp, zp, yp, M, N, K, act, none, ws, locks, splits);                                    \
-        else if (splits > 1 && xlds && wide)                                                                   \
-            mma_kernel<WK, U, T, 1, kXLdsWide, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, \
-                                                                                      act, none, ws, locks, splits); \
-        else if (splits > 1 && xlds)                                                                           \
-            mma_kernel<WK, U, T, 1, kXLds, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, \
-                                                                                  none, ws, locks, splits);    \
-        else if (splits > 1)                                                                                   \
-            mma_kernel<WK, U, T, 1, kXGlobal, false, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, \
-                                                                                     act, none, ws, locks, splits); \
-        else if (nin)                                                                                          \
-            mma_kernel<WK, U, T, 1, kXLds, true><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, *nin, \
-                                                                             ws, locks, splits);               \
-        else if (xlds && wide)                                                                                 \
-            mma_kernel<WK, U, T, 1, kXLdsWide><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none, \
-                                                                          ws, locks, splits);                  \
-        else if (xlds)                                                                                         \
-            mma_kernel<WK, U, T, 1, kXLds><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none, ws, \
-                                                                      locks, splits);                          \
-        else if (mt == 1)                                                                                      \
-            mma_kernel<WK, U, T, 1, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
-                                                                         ws, locks, splits);                   \
-        else if (mt == 2)                                                                                      \
-            mma_kernel<WK, U, T, 2, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
-                                                                         ws, locks, splits);                   \
-        else                                                                                                   \
-            mma_kernel<WK, U, T, 4, kXGlobal><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, yp, M, N, K, act, none,  \
-                                                                         ws, locks, splits);                   \
-        TW4_LAUNCH_CHECK("mma: launch");                                                                       \
-        return TW4_OK;                                                                                         \
+                                             static_cast<size_t>(kMaxLds));                                               \
+        const size_t lds = 16 * (static_cast<size_t>(                                                                     \
+                                     decode_lds(xlds, M, 128 * R, 0, red_u4, nin != nullptr).total) +                     \
+                                 1); /* + the split-K flag */                                                             \
+        const unsigned grid = static_cast<unsigned>(units);                                                               \
+        TW4_REQUIRE(per_cu == 0 || xlds, TW4_ECONFIG, "mma: the persistent form stages x in LDS (M = %d, K = %d)",        \
+                    M, K);                                                                                                \
+        if (per_cu > 0 && wide)                                                                                           \
+            mma_kernel<WK, U, T, 1, kXLdsWide, false, false, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));       \
+        else if (per_cu > 0)                                                                                              \
+            mma_kernel<WK, U, T, 1, kXLds, false, false, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));           \
+        else if (splits > 1 && xlds && wide)                                                                              \
+            mma_kernel<WK, U, T, 1, kXLdsWide, false, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));              \
+        else if (splits > 1 && xlds)                                                                                      \
+            mma_kernel<WK, U, T, 1, kXLds, false, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                  \
+        else if (splits > 1)                                                                                              \
+            mma_kernel<WK, U, T, 1, kXGlobal, false, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));               \
+        else if (nin)                                                                                                     \
+            mma_kernel<WK, U, T, 1, kXLds, true><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(*nin));                         \
+        else if (xlds && wide)                                                                                            \
+            mma_kernel<WK, U, T, 1, kXLdsWide><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                           \
+        else if (xlds)                                                                                                    \
+            mma_kernel<WK, U, T, 1, kXLds><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                               \
+        else if (mt == 1)                                                                                                 \
+            mma_kernel<WK, U, T, 1, kXGlobal><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                            \
+        else if (mt == 2)                                                                                                 \
+            mma_kernel<WK, U, T, 2, kXGlobal><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                            \
+        else                                                                                                              \
+            mma_kernel<WK, U, T, 4, kXGlobal><<<grid, WK * 64, lds, st>>>(TW4_MMA_ARGS(none));                            \
+        TW4_LAUNCH_CHECK("mma: launch");                                                                                  \
+        return TW4_OK;                                                                                                    \
     }
     TW4_DECODE_CONFIGS(TW4_MMA_CASE)
 #undef TW4_MMA_CASE
+#undef TW4_MMA_ARGS
     tw4host::set_error("mma: unsupported warps_k / unroll / ntile %d / %d / %d", warps_k, unroll, ntile);
     return TW4_ECONFIG;
 }
