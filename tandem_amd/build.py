@@ -36,11 +36,14 @@ def sources() -> list[str]:
 # - The MFMA accumulators sit in ordinary VGPRs instead of the accumulation registers: no
 #   v_accvgpr moves around each quant group's MFMAs. The persistent decode kernel on Qwen3-8B
 #   gate_up at M = 8 measured 13.9 -> 13.4 us (the others level).
-# - The first 16 kernel-argument dwords are preloaded into user SGPRs before a wavefront starts, so
-#   its first instructions do not wait on an s_load of the arguments. This shortens the start of
-#   the small decode grids: the GEMV on Qwen3-8B qkv at M = 1 measured 4.74 -> 4.39 us, the
-#   matrix-core kernels 1.5-3 % and the GEMV on the matrix cores 3-6 % at M = 2-16. gate_up's grid
-#   of 1536 workgroups is level.
+# - The leading kernel arguments are preloaded into user SGPRs before a wavefront starts (whole
+#   arguments, 13 dwords in these kernels), so its first instructions do not wait on an s_load of
+#   them. The decode kernels put what their prologue needs first and compute the grid size rather
+#   than read gridDim.x, a hidden argument past the preloaded ones. This shortens the start of the
+#   small decode grids: the GEMV on Qwen3-8B qkv at M = 1 measured 4.74 -> 4.39 us, the matrix-core
+#   kernels 1.5-3 % and the GEMV on the matrix cores 3-6 % at M = 2-16; with the grid computed,
+#   gate_up's GEMV at M = 1 10.3 -> 10.0 us. (The GEMM sources measured 1-5 % slower with the same
+#   preload and argument order at M = 32: their prologues still wait on the later arguments.)
 SOURCE_FLAGS = {"tw4_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
