@@ -747,13 +747,19 @@ def prof_main(argv=None) -> int:
     ap.add_argument("--summarize-counters", nargs="+", metavar="COUNTER_CSV",
                     help="per-dispatch medians of every counter of the profiled kernel, over one or more counter "
                          "passes of the same command, with busy shares per XCD (see summarize_counters)")
+    ap.add_argument("--probe", type=int, default=0, metavar="WORKGROUPS",
+                    help="after the projection's launches, as many launches of the plain-read probe "
+                         "(tw4_read_probe, grid-stride) over the projection's algorithmic bytes on this many "
+                         "workgroups: the same counters for a kernel that only reads (0: none)")
+    ap.add_argument("--kernel", default="", help="--summarize-counters: the kernel whose name contains this "
+                                                 "(e.g. read_probe), in place of the projection's")
     a = ap.parse_args(argv)
     k, n = PROF_SHAPES[a.proj]
     if a.summarize_mfma:
         print(json.dumps(summarize_mfma(a.summarize_mfma, a.m, n, k), indent=1))
         return 0
     if a.summarize_counters:
-        print(json.dumps(summarize_counters(a.summarize_counters, a.launches), indent=1))
+        print(json.dumps(summarize_counters(a.summarize_counters, a.launches, a.kernel), indent=1))
         return 0
     if a.summarize:
         alg = call_bytes(a.m, k, n) - (a.m * n if a.silu else 0)
@@ -804,9 +810,18 @@ def prof_run(a: argparse.Namespace) -> int:
     for i in range(a.launches):
         layers[i % copies](x)
     torch.cuda.synchronize()
+    kname, probe = kernel_of(awq, layers[0], a.m), ""
+    if a.probe > 0:  # the same bytes per launch, read and discarded, rotating over as many copies
+        nbytes = (call_bytes(a.m, k, n) - (a.m * n if layers[0].silu_mul else 0) + 15) // 16 * 16
+        del layers
+        bufs = [torch.ones(nbytes // 4, device=dev, dtype=torch.int32) for _ in range(copies)]
+        sink = torch.zeros(4, device=dev, dtype=torch.int32)
+        for i in range(a.launches):
+            w4_hip.read_probe(bufs[i % copies], sink, a.probe)
+        torch.cuda.synchronize()
+        probe = f", then {a.launches} read probes of {nbytes} bytes on {a.probe} workgroups"
     print(f"prof: {a.copies} copies of {a.copy_mib} MiB, {a.launches} x {a.proj} (K {k}, N {n}) M={a.m} "
-          f"over {copies} weight copies ({kernel_of(awq, layers[0], a.m)}), read calibration {a.read_gb} GB",
-          flush=True)
+          f"over {copies} weight copies ({kname}), read calibration {a.read_gb} GB{probe}", flush=True)
     return 0
 
 
@@ -902,9 +917,10 @@ def summarize_mfma(path: str, m: int, n: int, k: int) -> dict:
     return {"m": m, "n": n, "k": k, "kernels": rows}
 
 
-def summarize_counters(paths: list[str], launches: int) -> dict:
+def summarize_counters(paths: list[str], launches: int, kernel: str = "") -> dict:
     """The profiled kernel of `bench.py prof` counter runs (the tw4 kernel with exactly `launches`
-    dispatches, never a load-time repack): the median per dispatch of every counter in the given
+    dispatches, never a load-time repack; with `kernel`, the one whose name contains it, e.g. the
+    read probe of --probe): the median per dispatch of every counter in the given
     counter_collection.csv files (one per --pmc pass) and of the kernel duration, plus derived shares.
     The SQ counters and GRBM_GUI_ACTIVE are summed over the 8 XCDs, so GRBM_GUI_ACTIVE / 8 is the
     kernel's clock cycles and a busy share is cycles / (cycles x 1024 SIMDs):
@@ -925,6 +941,7 @@ def summarize_counters(paths: list[str], launches: int) -> dict:
                 rows.setdefault(row["Kernel_Name"], []).append(row)
         cands = [k for k in rows if "tw4" in k and not any(t in k for t in LOAD_TIME_KERNELS)
                  and len({r["Dispatch_Id"] for r in rows[k]}) == launches]
+        cands = [k for k in cands if kernel in k] if kernel else [k for k in cands if "read_probe" not in k]
         if len(cands) != 1:
             raise SystemExit(f"{path}: {len(cands)} tw4 kernels with {launches} dispatches: {cands}")
         name = cands[0]
