@@ -650,7 +650,12 @@ def tune_main(argv=None) -> int:
         for m in (int(v) for v in a.ms.split(",")):
             x = torch.randn(m, k, device=dev, dtype=torch.float16)
             res = {}
-            for cfg in w4_hip.decode_configs():
+            decode = w4_hip.decode_configs()
+            for cfg in w4_hip.mma_configs():  # the decode configs, then the row-tile-wide ones (mma only)
+                if cfg not in decode:
+                    if "mma" in kinds and m <= 64:
+                        attempt(res, ("mma", *cfg), [lambda w=w, c=cfg: ext.w4_mma(x, *w, *c, act) for w in ws])
+                    continue
                 if "gemv" in kinds and m <= 4:
                     attempt(res, ("gemv", *cfg), [lambda w=w, c=cfg: ext.w4_gemv(x, *w, *c, act) for w in ws])
                 if "gemvn" in kinds and m <= 4:  # the GEMV with the add + RMSNorm prologue (tw4_decode_norm)

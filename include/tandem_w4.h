@@ -125,7 +125,10 @@ int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint16_t* resid
 /* Decode on the matrix cores (v_mfma_f32_16x16x32_f16, weights as the A operand, the batch on
  * the 16-column side, ceil(M / 16) column tiles), 1 <= M <= 64; unroll * ceil(M / 16) <= 4.
  * act = 1: y = silu(gate) * up, [M, N/2], rows in interleave_gate_up order (N % 16 == 0);
- * act = 0: y [M, N].
+ * act = 0: y [M, N]. Configurations: those of tw4_decode_configs, and the row-tile-wide ones of
+ * tw4_mma_wide_configs (up to six row tiles per workgroup, x read from global memory at every
+ * chunk instead of staged in LDS; tw4_mma only: tw4_mma_splitk with splits > 1, tw4_mma_persist and
+ * tw4_decode_norm refuse them with TW4_ECONFIG).
  * Replaces w4_mma (python/tandem/csrc/w4_gemv.cu:166-295, 619-648). */
 int tw4_mma(const uint16_t* x, const int32_t* packed, const uint16_t* scales,
             const uint16_t* zeros, uint16_t* y, int M, int N, int K,
@@ -264,6 +267,11 @@ int tw4_read_probe(const void* src, int64_t bytes, int workgroups, int chunked, 
  * stages 3 the fourth value is the wavefronts along M). */
 int tw4_decode_configs(int* out, int max_configs);
 int tw4_gemm_configs(int* out, int max_configs);
+
+/* The row-tile-wide (warps_k, unroll, ntile) configurations tw4_mma takes besides
+ * tw4_decode_configs' (see tw4_mma). No reference counterpart: the reference's w4_mma compiles
+ * (warps_k, ntile) in {1, 2, 4} x {1, 2} (python/tandem/csrc/w4_gemv.cu:641-645). */
+int tw4_mma_wide_configs(int* out, int max_configs);
 
 /* Grid the last tw4_gemm call on this thread launched: workgroups, data-parallel tiles and
  * split factor (for benchmarks and tests; the reference keeps these internal,

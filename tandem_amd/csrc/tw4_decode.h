@@ -572,6 +572,13 @@ __global__ void __launch_bounds__(WK * 64) gemv_kernel(const h1* __restrict__ x,
     X(1, 4, 1) X(1, 8, 1) X(2, 4, 1) X(2, 8, 1) X(4, 1, 1) X(4, 2, 1) X(4, 4, 1) X(4, 8, 1) X(8, 1, 1) \
     X(8, 2, 1) X(8, 4, 1) X(16, 1, 1) X(16, 2, 1) X(2, 4, 2) X(4, 2, 2) X(4, 4, 2) X(8, 1, 2) X(8, 2, 2)
 
+// Row-tile-wide configurations of the matrix-core decode kernel only (warps_k, unroll, ntile): up to
+// six row tiles per workgroup, x read from global memory (L2) at every chunk and never staged in LDS,
+// so each wavefront's x fragments feed ntile weight blocks and no workgroup pays a staging phase. For
+// projections with many row tiles (gate_up): measured on Qwen3-8B gate_up, (4, 1, 6) at M = 32 took
+// 17.9-18.6 us against 20.2-21.2 us for the x-ring GEMM, (4, 1, 3) at M = 8 12.5 against 13.1 us.
+#define TW4_MMA_WIDE_CONFIGS(X) X(4, 1, 2) X(4, 1, 3) X(4, 1, 6) X(4, 2, 3)
+
 constexpr int kMaxDevices = 64;
 constexpr int kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
 constexpr int kXLdsLimit = 80 * 1024;    // mma keeps x in LDS up to this size (M = 8 at K = 4096)

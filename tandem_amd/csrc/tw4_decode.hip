@@ -435,6 +435,108 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     }
 }
 
+// The row-tile-wide configurations (TW4_MMA_WIDE_CONFIGS) in a kernel of their own: x from global
+// memory, one tile group of NT row tiles per workgroup, the epilogue chosen at compile time (ACT:
+// SwiGLU). Its chunks are mma_chunk's; it has none of mma_kernel's other forms (x in LDS, the fused
+// norm, split-K, the persistent loop), whose state changed the compiler's schedule of the same
+// chunk loop: that kernel's loop waited for two more loads per group than this one's, and ran
+// Qwen3-8B gate_up at M = 24 in 17.6 us kernel-only against 16.2 us here.
+template <int WK, int U, int NT, int MT, bool ACT>
+__global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
+                                                          const h1* __restrict__ scales, const h1* __restrict__ zeros,
+                                                          int M, int N, int K, int nunits, h1* __restrict__ y) {
+    extern __shared__ u4 smem[];  // [WK - 1][NT][MT][64] f4 partial sums
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
+    const int r = lane & 15, kb = lane >> 4;
+    const int G = K >> 7, tiles = (N + 15) >> 4;
+    const int tile0 = xcd_rotated_block(nunits) * NT;
+    const uint32_t magic = magic_reg();
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(scales);
+    const uint16_t* z16 = reinterpret_cast<const uint16_t*>(zeros);
+    const TileStreams<NT> ts = tile_streams<NT>(w, s16, z16, tile0, tiles, N, G, lane);
+    const h8* xl[MT];
+#pragma unroll
+    for (int b = 0; b < MT; ++b)
+        xl[b] = reinterpret_cast<const h8*>(x + static_cast<int64_t>(min(16 * b + r, M - 1)) * K + 32 * kb);
+    const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
+    const int nch = (ge - gb + U - 1) / U;
+    const DecodeLds l{};  // unused by the global-x chunks
+    WeightSet<U, NT> a, b;
+    load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
+    f4 acc[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    int i = 0;
+    for (; i + 2 < nch; i += 2) {
+        mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc, gb + U * i,
+                                             ge, 0, kb, magic);
+        mma_chunk<true, kXGlobal, U, NT, MT>(b, a, ts, gb + U * (i + 2), s16, z16, smem, l, xl, 0, acc,
+                                             gb + U * (i + 1), ge, 0, kb, magic);
+    }
+    if (i + 2 == nch) {
+        mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc, gb + U * i,
+                                             ge, 0, kb, magic);
+        mma_chunk<false, kXGlobal, U, NT, MT>(b, a, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * (i + 1), ge, 0, kb,
+                                              magic);
+    } else if (i + 1 == nch) {
+        mma_chunk<false, kXGlobal, U, NT, MT>(a, b, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * i, ge, 0, kb, magic);
+    }
+    if (WK > 1) {
+        f4* red = reinterpret_cast<f4*>(smem);
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int bb = 0; bb < MT; ++bb) red[(((wave - 1) * NT + t) * MT + bb) * 64 + lane] = acc[t][bb];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int v = 0; v < WK - 1; ++v)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int bb = 0; bb < MT; ++bb) acc[t][bb] += red[((v * NT + t) * MT + bb) * 64 + lane];
+    }
+    if constexpr (ACT) {  // N % 16 == 0 (checked on the host): gate rows 4 kb + i, up rows in lane + 32
+        const int half_n = N >> 1;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = tile0 + t;
+#pragma unroll
+            for (int bb = 0; bb < MT; ++bb) {
+                f4 up;
+                up.x = lane_xor32(acc[t][bb].x, lane);
+                up.y = lane_xor32(acc[t][bb].y, lane);
+                up.z = lane_xor32(acc[t][bb].z, lane);
+                up.w = lane_xor32(acc[t][bb].w, lane);
+                const int m = 16 * bb + r;
+                if (kb >= 2 || m >= M || tt >= tiles) continue;
+                const f4 g4 = acc[t][bb];
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * half_n + 8 * tt + 4 * kb) =
+                    h4{static_cast<h1>(silu(g4.x) * up.x), static_cast<h1>(silu(g4.y) * up.y),
+                       static_cast<h1>(silu(g4.z) * up.z), static_cast<h1>(silu(g4.w) * up.w)};
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int n = 16 * (tile0 + t) + 4 * kb;  // N % 8 == 0: n < N implies n + 3 < N
+            if (n >= N) continue;
+#pragma unroll
+            for (int bb = 0; bb < MT; ++bb) {
+                const int m = 16 * bb + r;
+                if (m >= M) continue;
+                const f4 a4 = acc[t][bb];
+                *reinterpret_cast<h4*>(y + static_cast<int64_t>(m) * N + n) =
+                    h4{static_cast<h1>(a4.x), static_cast<h1>(a4.y), static_cast<h1>(a4.z), static_cast<h1>(a4.w)};
+            }
+        }
+    }
+}
+
 static int g_decode_ready[kMaxDevices];
 static int g_decode_cus[kMaxDevices];
 
@@ -470,6 +572,14 @@ int decode_prepare(int dev) {
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 2, kXGlobal>);      \
     if (rc == TW4_OK) rc = allow_lds(mma_kernel<WK, U, T, 4, kXGlobal>);
     TW4_DECODE_CONFIGS(TW4_ATTR)
+#define TW4_ATTR_WIDE_ACT(WK, U, T, A)                                       \
+    if (rc == TW4_OK) rc = allow_lds(mma_wide_kernel<WK, U, T, 1, A>);        \
+    if (rc == TW4_OK) rc = allow_lds(mma_wide_kernel<WK, U, T, 2, A>);        \
+    if (rc == TW4_OK) rc = allow_lds(mma_wide_kernel<WK, U, T, 4, A>);
+#define TW4_ATTR_WIDE(WK, U, T) TW4_ATTR_WIDE_ACT(WK, U, T, false) TW4_ATTR_WIDE_ACT(WK, U, T, true)
+    TW4_MMA_WIDE_CONFIGS(TW4_ATTR_WIDE)
+#undef TW4_ATTR_WIDE
+#undef TW4_ATTR_WIDE_ACT
 #undef TW4_ATTR
 #undef TW4_ATTR_GEMV
     if (rc == TW4_OK) g_decode_ready[dev] = 1;
@@ -657,6 +767,34 @@ int mma_launch(const h1* xp, const u4* wp, const h1* sp, const h1* zp, h1* yp, i
     }
     TW4_DECODE_CONFIGS(TW4_MMA_CASE)
 #undef TW4_MMA_CASE
+// The row-tile-wide configurations: x from global memory at any M, one workgroup per tile group.
+#define TW4_WIDE_LAUNCH(WK, U, T, MTV, A)                                                                     \
+    mma_wide_kernel<WK, U, T, MTV, A><<<grid, WK * 64, lds, st>>>(xp, wp, sp, zp, M, N, K, static_cast<int>(grid), yp)
+#define TW4_MMA_WIDE_CASE(WK, U, T)                                                                           \
+    if (warps_k == WK && unroll == U && ntile == T) {                                                         \
+        TW4_REQUIRE(splits == 1 && per_cu == 0 && !nin, TW4_ECONFIG,                                         \
+                    "mma: (%d, %d, %d) reads x from global memory: no split-K, persistent form or fused norm", \
+                    WK, U, T);                                                                                \
+        const size_t lds = 16 * static_cast<size_t>((WK - 1) * T * mt * 64);                                  \
+        const unsigned grid = static_cast<unsigned>(units);                                                   \
+        if (mt == 1 && act)                                                                                   \
+            TW4_WIDE_LAUNCH(WK, U, T, 1, true);                                                               \
+        else if (mt == 1)                                                                                     \
+            TW4_WIDE_LAUNCH(WK, U, T, 1, false);                                                              \
+        else if (mt == 2 && act)                                                                              \
+            TW4_WIDE_LAUNCH(WK, U, T, 2, true);                                                               \
+        else if (mt == 2)                                                                                     \
+            TW4_WIDE_LAUNCH(WK, U, T, 2, false);                                                              \
+        else if (act)                                                                                         \
+            TW4_WIDE_LAUNCH(WK, U, T, 4, true);                                                               \
+        else                                                                                                  \
+            TW4_WIDE_LAUNCH(WK, U, T, 4, false);                                                              \
+        TW4_LAUNCH_CHECK("mma: launch");                                                                      \
+        return TW4_OK;                                                                                        \
+    }
+    TW4_MMA_WIDE_CONFIGS(TW4_MMA_WIDE_CASE)
+#undef TW4_MMA_WIDE_CASE
+#undef TW4_WIDE_LAUNCH
 #undef TW4_MMA_ARGS
     tw4host::set_error("mma: unsupported warps_k / unroll / ntile %d / %d / %d", warps_k, unroll, ntile);
     return TW4_ECONFIG;
@@ -757,8 +895,6 @@ extern "C" int tw4_decode_norm(const uint16_t* x, const uint16_t* residual, uint
     }
 }
 
-extern "C" int tw4_decode_configs(int* out, int max_configs) {
-    int n = 0;
 #define TW4_LIST(WK, U, T)                  \
     if (out && n < max_configs) {           \
         out[3 * n] = WK;                    \
@@ -766,7 +902,16 @@ extern "C" int tw4_decode_configs(int* out, int max_configs) {
         out[3 * n + 2] = T;                 \
     }                                       \
     ++n;
+
+extern "C" int tw4_decode_configs(int* out, int max_configs) {
+    int n = 0;
     TW4_DECODE_CONFIGS(TW4_LIST)
-#undef TW4_LIST
     return n;
 }
+
+extern "C" int tw4_mma_wide_configs(int* out, int max_configs) {
+    int n = 0;
+    TW4_MMA_WIDE_CONFIGS(TW4_LIST)
+    return n;
+}
+#undef TW4_LIST

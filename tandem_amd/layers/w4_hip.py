@@ -53,6 +53,7 @@ _SIGNATURES = {
     "tw4_gemm_last_grid": ([ctypes.POINTER(_I)] * 3, _I),
     "tw4_read_probe": ([_P, _I64, _I, _I, _I, ctypes.c_uint32, _P, _P], _I),
     "tw4_decode_configs": ([ctypes.POINTER(_I), _I], _I),
+    "tw4_mma_wide_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemm_configs": ([ctypes.POINTER(_I), _I], _I),
     "tw4_gemv_f16": ([_P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "tw4_gemv_f16_configs": ([ctypes.POINTER(_I), _I], _I),
@@ -86,6 +87,17 @@ def _configs(name: str, width: int) -> tuple[tuple[int, ...], ...]:
 def decode_configs() -> tuple[tuple[int, int, int], ...]:
     """The compiled (warps_k, unroll, ntile) configurations of w4_gemv / w4_mma."""
     return _configs("tw4_decode_configs", 3)
+
+
+def mma_wide_configs() -> tuple[tuple[int, int, int], ...]:
+    """The row-tile-wide (warps_k, unroll, ntile) configurations only w4_mma takes (x read from global
+    memory, up to six row tiles per workgroup; no split-K, persistent form or fused norm)."""
+    return _configs("tw4_mma_wide_configs", 3)
+
+
+def mma_configs() -> tuple[tuple[int, int, int], ...]:
+    """Every (warps_k, unroll, ntile) configuration w4_mma takes."""
+    return decode_configs() + mma_wide_configs()
 
 
 def gemm_configs() -> tuple[tuple[int, int, int, int, int], ...]:

@@ -25,6 +25,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SHAPES = ((128, 24), (256, 520), (1024, 64), (4096, 1000))  # (K, N); N % 16 != 0 exercises the padded tile
 DECODE_CONFIGS = w4_hip.decode_configs()  # every compiled (warps_k, unroll, ntile)
+MMA_CONFIGS = w4_hip.mma_configs()        # those and the row-tile-wide ones only w4_mma takes
 GEMM_CONFIGS = w4_hip.gemm_configs()      # every compiled (MT, NT, WARPS_N, WARPS_K, STAGES)
 
 
@@ -224,14 +225,15 @@ def test_decode_norm_small_k_against_oracle(ext):
 
 
 def test_mma_every_config(ext):
-    """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229)."""
+    """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229),
+    the row-tile-wide ones included (a partial last group of six row tiles at N = 520 and 1000)."""
     for k, n in SHAPES:
         c = Case(k, n, seed=4)
         for m in range(1, 17):
             x = c.x(m, seed=200 + m)
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
-            for cfg in DECODE_CONFIGS:
+            for cfg in MMA_CONFIGS:
                 check_close(ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0), ref, 0.02, 0.01, (k, n, m, cfg), "mma")
 
 
@@ -249,7 +251,7 @@ def test_mma_wide_batches(ext):
             x = c.x(m, seed=600 + m)
             ref = o.linear(x, c.w_exact)
             xg = gpu(x)
-            for cfg in DECODE_CONFIGS:
+            for cfg in MMA_CONFIGS:
                 if not _wide_ok(cfg, m):
                     with pytest.raises(RuntimeError):
                         ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0)
@@ -264,7 +266,7 @@ def test_mma_wide_silu_mul(ext):
             x = c.x(m, seed=700 + m)
             ref = o.swiglu_reference(x, c.w_exact)
             xg = gpu(x)
-            for cfg in DECODE_CONFIGS:
+            for cfg in MMA_CONFIGS:
                 if _wide_ok(cfg, m):
                     y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
                     assert y.shape == (m, n // 2)
@@ -279,10 +281,35 @@ def test_mma_silu_mul(ext):
             x = c.x(m, seed=300 + m)
             ref = o.swiglu_reference(x, c.w_exact)
             xg = gpu(x)
-            for cfg in DECODE_CONFIGS:
+            for cfg in MMA_CONFIGS:
                 y = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 1)
                 assert y.shape == (m, n // 2)
                 check_close(y, ref, 0.02, 0.01, (k, n, m, cfg), "mma")
+
+
+def test_mma_row_tile_wide_configs_refuse_the_other_forms(ext):
+    """The row-tile-wide configs read x from global memory: the split-K, persistent and fused-norm
+    entries refuse them with an error (nothing is launched); tw4_mma with splits = 1 takes them."""
+    buf, locks = w4_hip.workspace(DEV)
+    c = Case(1024, 512, seed=31)
+    x = c.x(4, seed=31)
+    xg = gpu(x)
+    nw = torch.ones(1024, dtype=torch.float16, device=DEV)
+    for cfg in w4_hip.mma_wide_configs():
+        assert cfg not in DECODE_CONFIGS
+        with pytest.raises(RuntimeError, match="reads x from global memory"):
+            ext.w4_mma_splitk(xg, c.packed, c.s, c.zz, buf, locks, *cfg, 2, 0)
+        with pytest.raises(RuntimeError, match="reads x from global memory"):
+            ext.w4_mma_persist(xg, c.packed, c.s, c.zz, *cfg, 1, 0)
+        with pytest.raises(RuntimeError, match="reads x from global memory"):
+            ext.w4_decode_norm(xg, None, nw, 1e-6, c.packed, c.s, c.zz, 1, *cfg, 0)
+        with pytest.raises(RuntimeError):  # not a GEMV configuration
+            ext.w4_gemv(xg, c.packed, c.s, c.zz, *cfg, 0)
+        one = ext.w4_mma(xg, c.packed, c.s, c.zz, *cfg, 0)
+        assert torch.equal(one, ext.w4_mma_splitk(xg, c.packed, c.s, c.zz, buf, locks, *cfg, 1, 0))
+        check_close(one, o.linear(x, c.w_exact), 0.02, 0.01, (1024, 512, 4, cfg), "mma")
+    torch.cuda.synchronize()
+    assert int(locks.abs().sum()) == 0
 
 
 def test_mma_split_k_every_config(ext):

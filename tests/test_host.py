@@ -49,9 +49,12 @@ def test_config_queries():
     assert all(c[3] in ((4, 8) if c[4] == 1 else (1, 2)) for c in gemm)
     assert {c[4] for c in gemm} == {0, 1, 2, 3}
     assert awq.DEFAULT_KERNEL[1:] in dec
+    wide = w4_hip.mma_wide_configs()
+    assert wide and not set(wide) & set(dec) and all(len(c) == 3 and 2 <= c[2] <= 6 for c in wide)
+    assert w4_hip.mma_configs() == dec + wide
     for m_max, cfg in awq.DEFAULT_GEMM:
         if cfg is not None and cfg[0] == "mma":
-            assert tuple(cfg[1:]) in dec and m_max <= 64
+            assert tuple(cfg[1:]) in dec + wide and m_max <= 64
         elif cfg is not None:
             assert cfg[:5] in gemm
 
@@ -255,6 +258,7 @@ def test_kernel_for_follows_the_tables():
 def test_tables_are_well_formed():
     assert awq.DEFAULT_KERNEL[0] in ("gemv", "mma") and len(awq.DEFAULT_KERNEL) == 4
     decode = set(w4_hip.decode_configs())
+    mma = set(w4_hip.mma_configs())  # w4_mma also takes the row-tile-wide configs
     gemm = set(w4_hip.gemm_configs())
     for table in awq.W4_KERNELS.values():
         for key, cfg in table.items():
@@ -272,7 +276,7 @@ def test_tables_are_well_formed():
                 assert len(cfg) == 5 and tuple(cfg[1:4]) in decode and 1 <= cfg[4] <= 8
                 assert m * (2 * k + 16) <= 136 * 1024  # past 80 KB only for grids of at most one per CU
             else:  # a compiled decode config; gemv only where it runs (M <= 4), gemvm where x' fits LDS
-                assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in decode
+                assert cfg[0] in ("gemv", "gemvm", "mma") and tuple(cfg[1:]) in (mma if cfg[0] == "mma" else decode)
                 assert cfg[0] != "gemv" or m <= 4
                 assert cfg[0] != "gemvm" or m * (2 * k + 16) + m * (k // 128) * 36 <= 160 * 1024
     for ladder in [awq.DEFAULT_GEMM, *[v for t in awq.W4_GEMM_KERNELS.values() for v in t.values()]]:
@@ -280,7 +284,7 @@ def test_tables_are_well_formed():
         assert m_maxes == sorted(m_maxes)
         for m_max, cfg in ladder:
             assert cfg is None or (len(cfg) == 6 and tuple(cfg[:5]) in gemm) or \
-                (cfg[0] == "mma" and tuple(cfg[1:]) in decode and m_max <= 64 and cfg[2] * -(-m_max // 16) <= 4)
+                (cfg[0] == "mma" and tuple(cfg[1:]) in mma and m_max <= 64 and cfg[2] * -(-m_max // 16) <= 4)
 
 
 def test_norm_entry_lookup():
