@@ -445,6 +445,9 @@ template <int WK, int U, int NT, int MT, bool ACT>
 __global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                           const h1* __restrict__ scales, const h1* __restrict__ zeros,
                                                           int M, int N, int K, int nunits, h1* __restrict__ y) {
+    if constexpr (U * MT > 4 && MT > 1) {
+        return;  // register budget: never launched (tw4_mma rejects U * MT > 4 for M > 16)
+    } else {
     extern __shared__ u4 smem[];  // [WK - 1][NT][MT][64] f4 partial sums
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR
     const int r = lane & 15, kb = lane >> 4;
@@ -535,6 +538,7 @@ __global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict_
             }
         }
     }
+}
 }
 
 static int g_decode_ready[kMaxDevices];
