@@ -744,7 +744,8 @@ def prof_main(argv=None) -> int:
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--read-gb", type=float, default=0.0, help="plain-read calibration size (0: none)")
     ap.add_argument("--silu", action="store_true", help="gate_up with the SwiGLU epilogue")
-    ap.add_argument("--cfg", default="", help="GEMM config mt,nt,warps_n,warps_k,stages,splits for every M > 16")
+    ap.add_argument("--cfg", default="", help="GEMM config mt,nt,warps_n,warps_k,stages,splits (or a ladder's "
+                                              "mma rung, mma,warps_k,unroll,ntile) for every M > 16")
     ap.add_argument("--decode", default="", help="decode-table entry kind,args for M <= 16 (e.g. gemv,4,2,2 or "
                                                  "mmap,8,1,2,2), in place of the table's")
     ap.add_argument("--summarize", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
@@ -804,7 +805,9 @@ def prof_run(a: argparse.Namespace) -> int:
         lin = random_linear(torch, awq, k, n, dev, g, silu=a.silu and a.proj == "gate_up")
         if a.cfg:  # a per-layer copy: the module-level table is shared by every W4Linear
             key = (n, k) + (("silu",) if lin.silu_mul else ())
-            lin.gemm_kernels = {**lin.gemm_kernels, key: ((1 << 30, tuple(int(v) for v in a.cfg.split(","))),)}
+            head, *rest = a.cfg.split(",")
+            cfg = ("mma", *(int(v) for v in rest)) if head == "mma" else tuple(int(v) for v in a.cfg.split(","))
+            lin.gemm_kernels = {**lin.gemm_kernels, key: ((1 << 30, cfg),)}
         if a.decode:
             kind, *args = a.decode.split(",")
             key = (n, k, a.m) + (("silu",) if lin.silu_mul else ())
