@@ -269,8 +269,10 @@ int tw4_decode_configs(int* out, int max_configs);
 int tw4_gemm_configs(int* out, int max_configs);
 
 /* The row-tile-wide (warps_k, unroll, ntile) configurations tw4_mma takes besides
- * tw4_decode_configs' (see tw4_mma). No reference counterpart: the reference's w4_mma compiles
- * (warps_k, ntile) in {1, 2, 4} x {1, 2} (python/tandem/csrc/w4_gemv.cu:641-645). */
+ * tw4_decode_configs' (see tw4_mma). The reference's w4_mma compiles ntile 1 and 2 only
+ * (python/tandem/csrc/w4_gemv.cu:641-645): (4, 1, 3), (4, 1, 6) and (4, 2, 3) have no counterpart
+ * there; (4, 1, 2) is one of its configurations, which this library runs in the row-tile-wide
+ * form. */
 int tw4_mma_wide_configs(int* out, int max_configs);
 
 /* Grid the last tw4_gemm call on this thread launched: workgroups, data-parallel tiles and
