@@ -435,12 +435,69 @@ __global__ void __launch_bounds__(WK * 64) mma_kernel(const h1* __restrict__ x, 
     }
 }
 
+// One chunk's x fragments read from global memory (k = 128 g + 32 kb + 8 s .. + 7 of batch rows
+// 16 b + r), per lane.
+template <int U, int MT>
+struct XFrags {
+    h8 v[U][4][MT];
+};
+
+template <int U, int MT>
+__device__ __forceinline__ void load_x_frags(XFrags<U, MT>& xf, const h8* const (&xl)[MT], int g0, int glast) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = min(g0 + u, glast);  // past the range: a valid address; the group is not added
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int b = 0; b < MT; ++b) xf.v[u][s][b] = xl[b][16 * g + s];
+    }
+}
+
+// mma_chunk's arithmetic with the chunk's x fragments loaded one chunk ahead, beside its weights:
+// PF loads the next chunk's weights and x together, so the x loads' L2 round trip is hidden behind
+// this chunk's math like the weights' instead of being waited for at the start of every chunk. The
+// same sums in the same order as mma_chunk (the same bits). Used by the six-row-tile configuration,
+// whose grid has one wavefront per SIMD on Qwen3-8B gate_up (no other wavefront's math covers that
+// round trip): M = 16-32 3-4 % faster. With two or three row tiles (two wavefronts per SIMD) it was
+// level at M = 8 and 2-5 % slower at M = 16-32, so those keep mma_chunk.
+template <bool PF, int U, int NT, int MT>
+__device__ __forceinline__ void mma_chunk_gx(const WeightSet<U, NT>& cur, WeightSet<U, NT>& nxt,
+                                             const XFrags<U, MT>& xcur, XFrags<U, MT>& xnxt,
+                                             const TileStreams<NT>& ts, const h8* const (&xl)[MT], const uint16_t* s16,
+                                             const uint16_t* z16, f4 (&acc)[NT][MT], int g0, int ge, uint32_t magic) {
+    if constexpr (PF) {
+        load_chunk<U, NT>(nxt, ts, s16, z16, g0 + U, ge - 1);
+        load_x_frags<U, MT>(xnxt, xl, g0 + U, ge - 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads above the math: the scheduler would sink them
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const bool valid = PF || g0 + u < ge;  // a chunk that prefetches has all its groups in range
+        GroupQ p[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            uint32_t s_raw, z_raw;
+            scale_zero(cur.p[u][t], s_raw, z_raw);
+            p[t] = group_q_raw(s_raw, z_raw, valid);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const h8 wa = dequant_word(word_of(cur.w[u][t], s), p[t], magic);
+#pragma unroll
+                for (int b = 0; b < MT; ++b) acc[t][b] = mfma16x16x32(wa, xcur.v[u][s][b], acc[t][b]);
+            }
+    }
+}
+
 // The row-tile-wide configurations (TW4_MMA_WIDE_CONFIGS) in a kernel of their own: x from global
 // memory, one tile group of NT row tiles per workgroup, the epilogue chosen at compile time (ACT:
-// SwiGLU). Its chunks are mma_chunk's; it has none of mma_kernel's other forms (x in LDS, the fused
-// norm, split-K, the persistent loop), whose state changed the compiler's schedule of the same
-// chunk loop: that kernel's loop waited for two more loads per group than this one's, and ran
-// Qwen3-8B gate_up at M = 24 in 17.6 us kernel-only against 16.2 us here.
+// SwiGLU). Its chunks are mma_chunk's (mma_chunk_gx's at six row tiles); it has none of mma_kernel's
+// other forms (x in LDS, the fused norm, split-K, the persistent loop), whose state changed the
+// compiler's schedule of the same chunk loop: that kernel's loop waited for two more loads per group
+// than this one's, and ran Qwen3-8B gate_up at M = 24 in 17.6 us kernel-only against 16.2 us here.
 template <int WK, int U, int NT, int MT, bool ACT>
 __global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict__ x, const u4* __restrict__ w,
                                                           const h1* __restrict__ scales, const h1* __restrict__ zeros,
@@ -463,7 +520,6 @@ __global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict_
         xl[b] = reinterpret_cast<const h8*>(x + static_cast<int64_t>(min(16 * b + r, M - 1)) * K + 32 * kb);
     const int gw = (G + WK - 1) / WK, gb = min(wave * gw, G), ge = min(gb + gw, G);
     const int nch = (ge - gb + U - 1) / U;
-    const DecodeLds l{};  // unused by the global-x chunks
     WeightSet<U, NT> a, b;
     load_chunk<U, NT>(a, ts, s16, z16, gb, max(ge - 1, 0));
     f4 acc[NT][MT];
@@ -472,19 +528,36 @@ __global__ void __launch_bounds__(WK * 64) mma_wide_kernel(const h1* __restrict_
 #pragma unroll
         for (int bb = 0; bb < MT; ++bb) acc[t][bb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     int i = 0;
-    for (; i + 2 < nch; i += 2) {
-        mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc, gb + U * i,
-                                             ge, 0, kb, magic);
-        mma_chunk<true, kXGlobal, U, NT, MT>(b, a, ts, gb + U * (i + 2), s16, z16, smem, l, xl, 0, acc,
-                                             gb + U * (i + 1), ge, 0, kb, magic);
-    }
-    if (i + 2 == nch) {
-        mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc, gb + U * i,
-                                             ge, 0, kb, magic);
-        mma_chunk<false, kXGlobal, U, NT, MT>(b, a, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * (i + 1), ge, 0, kb,
-                                              magic);
-    } else if (i + 1 == nch) {
-        mma_chunk<false, kXGlobal, U, NT, MT>(a, b, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * i, ge, 0, kb, magic);
+    if constexpr (NT >= 6) {  // x one chunk ahead (mma_chunk_gx)
+        XFrags<U, MT> xa, xb;
+        load_x_frags<U, MT>(xa, xl, gb, max(ge - 1, 0));
+        for (; i + 2 < nch; i += 2) {
+            mma_chunk_gx<true, U, NT, MT>(a, b, xa, xb, ts, xl, s16, z16, acc, gb + U * i, ge, magic);
+            mma_chunk_gx<true, U, NT, MT>(b, a, xb, xa, ts, xl, s16, z16, acc, gb + U * (i + 1), ge, magic);
+        }
+        if (i + 2 == nch) {
+            mma_chunk_gx<true, U, NT, MT>(a, b, xa, xb, ts, xl, s16, z16, acc, gb + U * i, ge, magic);
+            mma_chunk_gx<false, U, NT, MT>(b, a, xb, xa, ts, xl, s16, z16, acc, gb + U * (i + 1), ge, magic);
+        } else if (i + 1 == nch) {
+            mma_chunk_gx<false, U, NT, MT>(a, b, xa, xb, ts, xl, s16, z16, acc, gb + U * i, ge, magic);
+        }
+    } else {  // x at the start of each chunk (mma_chunk)
+        const DecodeLds l{};  // unused by the global-x chunks
+        for (; i + 2 < nch; i += 2) {
+            mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc,
+                                                 gb + U * i, ge, 0, kb, magic);
+            mma_chunk<true, kXGlobal, U, NT, MT>(b, a, ts, gb + U * (i + 2), s16, z16, smem, l, xl, 0, acc,
+                                                 gb + U * (i + 1), ge, 0, kb, magic);
+        }
+        if (i + 2 == nch) {
+            mma_chunk<true, kXGlobal, U, NT, MT>(a, b, ts, gb + U * (i + 1), s16, z16, smem, l, xl, 0, acc,
+                                                 gb + U * i, ge, 0, kb, magic);
+            mma_chunk<false, kXGlobal, U, NT, MT>(b, a, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * (i + 1), ge,
+                                                  0, kb, magic);
+        } else if (i + 1 == nch) {
+            mma_chunk<false, kXGlobal, U, NT, MT>(a, b, ts, 0, s16, z16, smem, l, xl, 0, acc, gb + U * i, ge, 0, kb,
+                                                  magic);
+        }
     }
     if (WK > 1) {
         f4* red = reinterpret_cast<f4*>(smem);
