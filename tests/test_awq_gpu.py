@@ -224,6 +224,33 @@ def test_decode_norm_small_k_against_oracle(ext):
                     check_close(y, ref, atol, rtol, (k, n, m, cfg, k01), "norm")
 
 
+def test_gemv_one_group_ring_every_remainder(ext):
+    """The one-group GEMV configurations keep two groups in flight in three register sets; a
+    wavefront's last pass then covers 0-4 chunks after 0, 1 or more full passes of three. K = 128 G
+    with G = 3 .. 40 gives the wavefronts of warps_k 4, 8 and 16 every remainder, with and without a
+    full pass first (the SHAPES above reach only some), plain, SwiGLU and with the fused norm."""
+    ring = [cfg for cfg in DECODE_CONFIGS if cfg[1] == 1]
+    assert ring, "no one-group configuration compiled"
+    for g in (3, 5, 6, 7, 9, 10, 12, 13, 20, 24, 28, 36, 40):
+        k = 128 * g
+        c = Case(k, 48, seed=30 + g)
+        ci = Case(k, 32, seed=60 + g, interleave=True)
+        for m in (1, 3):
+            x = c.x(m, seed=1200 + 10 * g + m)
+            ref = o.linear(x, c.w_exact)
+            ref_act = o.swiglu_reference(x, ci.w_exact)
+            xn, r, w = _norm_inputs(m, k, seed=1300 + 10 * g + m)
+            a, r2 = o.add_rms_norm(xn, r, w, 1e-6)
+            ref_norm = o.linear(a, c.w_exact)
+            for cfg in ring:
+                check_close(ext.w4_gemv(gpu(x), c.packed, c.s, c.zz, *cfg), ref, 0.05, 0.02, (k, m, cfg), "gemv")
+                check_close(ext.w4_gemv(gpu(x), ci.packed, ci.s, ci.zz, *cfg, 1), ref_act, 0.05, 0.02, (k, m, cfg),
+                            "gemv")
+                y, r_out = ext.w4_decode_norm(gpu(xn), gpu(r), gpu(w), 1e-6, c.packed, c.s, c.zz, 0, *cfg, 0)
+                assert (r_out.cpu().numpy().view(np.uint16) == r2.view(np.uint16)).all()
+                check_close(y, ref_norm, 0.05, 0.02, (k, m, cfg), "norm")
+
+
 def test_mma_every_config(ext):
     """Matrix-core decode kernel, M = 1..16, every compiled config (tests/test_awq.py:217-229),
     the row-tile-wide ones included (a partial last group of six row tiles at N = 520 and 1000)."""
